@@ -1,0 +1,532 @@
+// C ABI of the attention hot path (include/bitgpu_attn.h): the KV-cache object, argument
+// validation, workspace management and kernel dispatch. Host code only; the kernels live in
+// kv_pack.hip, norm_rope.hip, decode.hip, prefill.hip and attn_f32.hip.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/bitgpu_attn.h"
+#include "bg_kernels.h"
+
+using bg::LayerView;
+
+struct bg_kv_cache {
+  int n_layers = 0, kv_heads = 0, D = 0, dtype = 0;
+  int capacity = 0;   // logical capacity (reference kvCapacity)
+  int cap = 0;        // physical slots (capacity rounded up to 32)
+  int max_seq = 0;
+  int roll = 0, sinks = 0, rope_abs = 0;
+  int head = 0;       // ring origin
+  int64_t evicted = 0;
+  std::vector<void*> k, v;
+  std::vector<float*> ks, vs;
+  const float* cos_tab = nullptr;
+  const float* sin_tab = nullptr;
+  int rope_positions = 0;
+  float* ws = nullptr;
+  size_t ws_floats = 0;
+  unsigned* ws_count = nullptr;
+  size_t ws_counters = 0;
+  int num_cus = 256;
+};
+
+namespace {
+
+thread_local std::string g_err;
+
+int32_t fail(int32_t code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = std::string("bitgpu: ") + buf;
+  return code;
+}
+
+int32_t hip_fail(hipError_t e, const char* what) {
+  if (e == hipErrorOutOfMemory) return fail(BG_E_OOM, "GPU out of memory during %s: %s", what, hipGetErrorString(e));
+  return fail(BG_E_DEVICE, "HIP error during %s: %s", what, hipGetErrorString(e));
+}
+
+int round32(int x) { return (x + 31) & ~31; }
+
+size_t elem_bytes(int dtype) { return (size_t)bg::kv_elem_bytes(dtype); }
+
+// Test hook: BG_FAULT_GROW_ALLOC=n makes the n-th device allocation inside bg_kv_grow fail,
+// so the rollback path can be exercised from the host without exhausting memory.
+hipError_t grow_malloc(void** p, size_t bytes, int* counter) {
+  const char* f = getenv("BG_FAULT_GROW_ALLOC");
+  (*counter)++;
+  if (f && atoi(f) == *counter) {
+    *p = nullptr;
+    return hipErrorOutOfMemory;
+  }
+  return hipMalloc(p, bytes);
+}
+
+LayerView view(const bg_kv_cache* c, int layer) {
+  LayerView L;
+  L.k = c->k[layer];
+  L.v = c->v[layer];
+  L.ks = c->dtype == BG_KV_Q8 ? c->ks[layer] : nullptr;
+  L.vs = c->dtype == BG_KV_Q8 ? c->vs[layer] : nullptr;
+  L.cap = c->cap;
+  L.kv_heads = c->kv_heads;
+  L.D = c->D;
+  L.dtype = c->dtype;
+  L.ring.roll = c->roll;
+  L.ring.sinks = c->sinks;
+  L.ring.W = c->max_seq - c->sinks;
+  L.ring.head = c->head;
+  L.max_seq = c->max_seq;
+  L.cos_tab = c->cos_tab;
+  L.sin_tab = c->sin_tab;
+  L.rope_positions = c->rope_positions;
+  L.rope_abs = c->rope_abs;
+  L.evicted = c->evicted;
+  return L;
+}
+
+void free_layers(std::vector<void*>& k, std::vector<void*>& v, std::vector<float*>& ks, std::vector<float*>& vs) {
+  for (auto p : k) if (p) (void)hipFree(p);
+  for (auto p : v) if (p) (void)hipFree(p);
+  for (auto p : ks) if (p) (void)hipFree(p);
+  for (auto p : vs) if (p) (void)hipFree(p);
+  k.clear(); v.clear(); ks.clear(); vs.clear();
+}
+
+// slots the caller may address: the window in sink mode, the grown capacity otherwise
+int addressable(const bg_kv_cache* c) { return c->roll ? c->max_seq : c->capacity; }
+
+}  // namespace
+
+extern "C" {
+
+const char* bg_last_error_message(void) { return g_err.c_str(); }
+
+const char* bg_version(void) { return "bitgpu-mi355x-attn 0.1.0 (gfx950)"; }
+
+int32_t bg_rope_tables(double theta, int32_t rot_dim, int32_t positions, double yarn_factor,
+                       int32_t yarn_original_max_positions, float* cos_out, float* sin_out) {
+  // synthRope, src/engine.ts:117-147: f64 inverse frequencies and angles, one f32 rounding
+  if (rot_dim <= 0 || (rot_dim & 1) || positions < 0 || !cos_out || !sin_out || !(theta > 0))
+    return fail(BG_E_INVALID, "bg_rope_tables: bad arguments (rot_dim %d, positions %d)", rot_dim, positions);
+  const int half = rot_dim / 2;
+  const double factor = yarn_factor > 1.0 ? yarn_factor : 1.0;
+  std::vector<double> inv(half);
+  double lo = 0, hi = 0;
+  if (factor != 1.0) {
+    const double orig = (double)yarn_original_max_positions;
+    lo = std::max(0.0, std::floor((rot_dim * std::log(orig / (32 * 2 * M_PI))) / (2 * std::log(theta))));
+    hi = std::min((double)(half - 1), std::ceil((rot_dim * std::log(orig / (2 * M_PI))) / (2 * std::log(theta))));
+  }
+  for (int j = 0; j < half; j++) {
+    const double pf = std::pow(theta, (2.0 * j) / rot_dim);
+    if (factor == 1.0) {
+      inv[j] = 1.0 / pf;
+    } else {
+      const double ramp = std::min(1.0, std::max(0.0, (j - lo) / (hi - lo)));
+      inv[j] = (1.0 / (factor * pf)) * ramp + (1.0 / pf) * (1 - ramp);
+    }
+  }
+  const double mscale = factor == 1.0 ? 1.0 : (double)(float)(0.1 * std::log(factor) + 1);
+  for (int p = 0; p < positions; p++)
+    for (int j = 0; j < half; j++) {
+      const double a = p * inv[j];
+      cos_out[(size_t)p * half + j] = (float)(std::cos(a) * mscale);
+      sin_out[(size_t)p * half + j] = (float)(std::sin(a) * mscale);
+    }
+  return BG_OK;
+}
+
+int32_t bg_evict_plan(int32_t fill, int32_t need, int32_t sinks, int32_t max_seq_len, int32_t* new_fill,
+                      int32_t* batch, int32_t* keep) {
+  // evict(), src/engine.ts:1188-1212
+  if (!new_fill || sinks < 0 || fill < sinks || max_seq_len <= sinks)
+    return fail(BG_E_INVALID, "bg_evict_plan: bad arguments (fill %d, sinks %d, max_seq %d)", fill, sinks, max_seq_len);
+  const int recent = fill - sinks;
+  const int quarter = (max_seq_len - sinks + 3) / 4;
+  const int b = std::min(recent, std::max(need, quarter));
+  const int k = recent - b;
+  *new_fill = k <= 0 ? sinks : sinks + k;
+  if (batch) *batch = b;
+  if (keep) *keep = k;
+  return BG_OK;
+}
+
+int32_t bg_stream_sync(void* stream) {
+  hipError_t e = stream ? hipStreamSynchronize((hipStream_t)stream) : hipDeviceSynchronize();
+  return e == hipSuccess ? BG_OK : hip_fail(e, "stream sync");
+}
+
+int32_t bg_kv_create(int32_t n_layers, int32_t kv_heads, int32_t head_dim, int32_t dtype, int32_t capacity,
+                     int32_t max_seq_len, int32_t roll, int32_t sinks, int32_t rope_pos_mode, bg_kv_cache** out) {
+  if (!out) return fail(BG_E_INVALID, "bg_kv_create: out is NULL");
+  *out = nullptr;
+  if (n_layers < 1 || kv_heads < 1 || max_seq_len < 1)
+    return fail(BG_E_INVALID, "bg_kv_create: n_layers %d, kv_heads %d, max_seq_len %d must be >= 1", n_layers, kv_heads, max_seq_len);
+  if (head_dim != 128 && head_dim != 256)
+    return fail(BG_E_UNSUPPORTED, "bg_kv_create: head_dim %d unsupported (128 or 256)", head_dim);
+  if (dtype != BG_KV_F32 && dtype != BG_KV_F16 && dtype != BG_KV_Q8)
+    return fail(BG_E_INVALID, "bg_kv_create: unknown kv dtype %d", dtype);
+  if (dtype == BG_KV_Q8 && head_dim % 32 != 0)  // src/engine.ts:372-373
+    return fail(BG_E_INVALID, "kvCache 'q8' needs head_dim divisible by 32 (got %d)", head_dim);
+  if (roll) {
+    if (sinks < 1) return fail(BG_E_INVALID, "bg_kv_create: sink mode needs sinks >= 1 (got %d)", sinks);
+    if (max_seq_len < sinks + 64)  // src/engine.ts:311-312
+      return fail(BG_E_INVALID, "overflow 'sinks' needs maxSeqLen >= sinkTokens + 64 (got %d with %d sinks)", max_seq_len, sinks);
+    if (rope_pos_mode != BG_ROPE_SLOT && rope_pos_mode != BG_ROPE_ABSOLUTE)
+      return fail(BG_E_INVALID, "bg_kv_create: unknown rope position mode %d", rope_pos_mode);
+  }
+  bg_kv_cache* c = new bg_kv_cache();
+  c->n_layers = n_layers;
+  c->kv_heads = kv_heads;
+  c->D = head_dim;
+  c->dtype = dtype;
+  c->max_seq = max_seq_len;
+  c->roll = roll ? 1 : 0;
+  c->sinks = roll ? sinks : 0;
+  c->rope_abs = roll && rope_pos_mode == BG_ROPE_ABSOLUTE;
+  // The ring needs the whole window resident; otherwise start at min(maxSeqLen, capacity)
+  // (KV_INITIAL = 512 when capacity <= 0, src/engine.ts:1044-1046) and grow by doubling.
+  int initial = capacity > 0 ? capacity : 512;
+  c->capacity = roll ? max_seq_len : std::min(max_seq_len, initial);
+  c->cap = round32(c->capacity);
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0) c->num_cus = cus;
+  const size_t row = (size_t)c->cap * kv_heads * head_dim * elem_bytes(dtype);
+  const size_t srow = (size_t)c->cap * kv_heads * (head_dim / 32) * sizeof(float);
+  for (int l = 0; l < n_layers; l++) {
+    void *kp = nullptr, *vp = nullptr;
+    float *ksp = nullptr, *vsp = nullptr;
+    hipError_t e = hipMalloc(&kp, row);
+    if (e == hipSuccess) e = hipMalloc(&vp, row);
+    if (e == hipSuccess && dtype == BG_KV_Q8) e = hipMalloc((void**)&ksp, srow);
+    if (e == hipSuccess && dtype == BG_KV_Q8) e = hipMalloc((void**)&vsp, srow);
+    c->k.push_back(kp);
+    c->v.push_back(vp);
+    c->ks.push_back(ksp);
+    c->vs.push_back(vsp);
+    if (e == hipSuccess) e = hipMemset(kp, 0, row);
+    if (e == hipSuccess) e = hipMemset(vp, 0, row);
+    if (e == hipSuccess && ksp) e = hipMemset(ksp, 0, srow);
+    if (e == hipSuccess && vsp) e = hipMemset(vsp, 0, srow);
+    if (e != hipSuccess) {
+      free_layers(c->k, c->v, c->ks, c->vs);
+      delete c;
+      return hip_fail(e, "KV cache allocation");
+    }
+  }
+  *out = c;
+  return BG_OK;
+}
+
+int32_t bg_kv_destroy(bg_kv_cache* c) {
+  if (!c) return BG_OK;
+  (void)hipDeviceSynchronize();
+  free_layers(c->k, c->v, c->ks, c->vs);
+  if (c->ws) (void)hipFree(c->ws);
+  if (c->ws_count) (void)hipFree(c->ws_count);
+  delete c;
+  return BG_OK;
+}
+
+int32_t bg_kv_capacity(const bg_kv_cache* c, int32_t* capacity) {
+  if (!c || !capacity) return fail(BG_E_INVALID, "bg_kv_capacity: NULL argument");
+  *capacity = c->capacity;
+  return BG_OK;
+}
+
+int32_t bg_kv_grow(bg_kv_cache* c, int32_t needed, void* stream) {
+  if (!c) return fail(BG_E_INVALID, "bg_kv_grow: NULL cache");
+  // ensureKvCapacity, src/engine.ts:1120-1178
+  needed = std::min(needed, c->max_seq);
+  if (needed <= c->capacity) return BG_OK;
+  const int newCap = std::min(c->max_seq, std::max(needed, c->capacity * 2));
+  const int ncap = round32(newCap);
+  hipStream_t st = (hipStream_t)stream;
+  const size_t eb = elem_bytes(c->dtype);
+  const size_t nrow = (size_t)ncap * c->kv_heads * c->D * eb;
+  const size_t nsrow = (size_t)ncap * c->kv_heads * (c->D / 32) * sizeof(float);
+  std::vector<void*> nk, nv;
+  std::vector<float*> nks, nvs;
+  int counter = 0;
+  hipError_t e = hipSuccess;
+  for (int l = 0; l < c->n_layers && e == hipSuccess; l++) {
+    void *kp = nullptr, *vp = nullptr;
+    float *ksp = nullptr, *vsp = nullptr;
+    e = grow_malloc(&kp, nrow, &counter);
+    if (e == hipSuccess) e = grow_malloc(&vp, nrow, &counter);
+    if (e == hipSuccess && c->dtype == BG_KV_Q8) e = grow_malloc((void**)&ksp, nsrow, &counter);
+    if (e == hipSuccess && c->dtype == BG_KV_Q8) e = grow_malloc((void**)&vsp, nsrow, &counter);
+    nk.push_back(kp);
+    nv.push_back(vp);
+    nks.push_back(ksp);
+    nvs.push_back(vsp);
+  }
+  if (e != hipSuccess) {
+    // roll back: keep the old buffers (src/engine.ts:1157-1173)
+    free_layers(nk, nv, nks, nvs);
+    (void)hipGetLastError();
+    return fail(BG_E_OOM, "KV cache growth to %d positions failed: %s", newCap, hipGetErrorString(e));
+  }
+  // copy every head's rows: [kvh][cap][...] regions keep their head stride = cap
+  for (int l = 0; l < c->n_layers && e == hipSuccess; l++) {
+    e = hipMemsetAsync(nk[l], 0, nrow, st);
+    if (e == hipSuccess) e = hipMemsetAsync(nv[l], 0, nrow, st);
+    if (e == hipSuccess && nks[l]) e = hipMemsetAsync(nks[l], 0, nsrow, st);
+    if (e == hipSuccess && nvs[l]) e = hipMemsetAsync(nvs[l], 0, nsrow, st);
+    for (int h = 0; h < c->kv_heads && e == hipSuccess; h++) {
+      const size_t ob = (size_t)c->cap * c->D * eb, nb = (size_t)ncap * c->D * eb;
+      e = hipMemcpyAsync((char*)nk[l] + h * nb, (char*)c->k[l] + h * ob, ob, hipMemcpyDeviceToDevice, st);
+      if (e == hipSuccess) e = hipMemcpyAsync((char*)nv[l] + h * nb, (char*)c->v[l] + h * ob, ob, hipMemcpyDeviceToDevice, st);
+      if (e == hipSuccess && nks[l]) {
+        const size_t os = (size_t)c->cap * (c->D / 32) * sizeof(float), ns = (size_t)ncap * (c->D / 32) * sizeof(float);
+        e = hipMemcpyAsync((char*)nks[l] + h * ns, (char*)c->ks[l] + h * os, os, hipMemcpyDeviceToDevice, st);
+        if (e == hipSuccess) e = hipMemcpyAsync((char*)nvs[l] + h * ns, (char*)c->vs[l] + h * os, os, hipMemcpyDeviceToDevice, st);
+      }
+    }
+  }
+  if (e == hipSuccess) e = st ? hipStreamSynchronize(st) : hipDeviceSynchronize();
+  if (e != hipSuccess) {
+    free_layers(nk, nv, nks, nvs);
+    return hip_fail(e, "KV cache growth copy");
+  }
+  free_layers(c->k, c->v, c->ks, c->vs);
+  c->k = nk;
+  c->v = nv;
+  c->ks = nks;
+  c->vs = nvs;
+  c->capacity = newCap;
+  c->cap = ncap;
+  return BG_OK;
+}
+
+int32_t bg_kv_set_rope(bg_kv_cache* c, const float* cos_tab, const float* sin_tab, int32_t positions, int32_t rot_dim) {
+  if (!c || !cos_tab || !sin_tab || positions < 1) return fail(BG_E_INVALID, "bg_kv_set_rope: bad arguments");
+  if (rot_dim != c->D) return fail(BG_E_UNSUPPORTED, "read-time rotation needs rot_dim == head_dim (%d vs %d)", rot_dim, c->D);
+  c->cos_tab = cos_tab;
+  c->sin_tab = sin_tab;
+  c->rope_positions = positions;
+  return BG_OK;
+}
+
+int32_t bg_kv_write(bg_kv_cache* c, int32_t layer, int32_t which, const float* src, int32_t rows, int32_t dst_row0,
+                    void* stream) {
+  if (!c || !src) return fail(BG_E_INVALID, "bg_kv_write: NULL argument");
+  if (layer < 0 || layer >= c->n_layers) return fail(BG_E_INVALID, "bg_kv_write: layer %d out of range", layer);
+  if (which != BG_K && which != BG_V) return fail(BG_E_INVALID, "bg_kv_write: which must be BG_K or BG_V");
+  if (rows < 0 || dst_row0 < 0) return fail(BG_E_INVALID, "bg_kv_write: negative rows/dst_row0");
+  const long last = (long)dst_row0 + rows;  // exclusive reference row
+  if (rows > 0 && (last + c->kv_heads - 1) / c->kv_heads > addressable(c))
+    return fail(BG_E_INVALID, "bg_kv_write: rows reach position %ld beyond capacity %d", (last - 1) / c->kv_heads, addressable(c));
+  hipError_t e = bg::launch_kv_write(view(c, layer), which, src, rows, dst_row0, (hipStream_t)stream);
+  return e == hipSuccess ? BG_OK : hip_fail(e, "kv write launch");
+}
+
+int32_t bg_qkv_prologue(bg_kv_cache* c, int32_t layer, const float* q, int32_t q_stride, const float* k, const float* v,
+                        int32_t S, int32_t H, const float* q_gamma, const float* k_gamma, float eps,
+                        const float* cos_tab, const float* sin_tab, int32_t rope_positions, int32_t rot_dim,
+                        int32_t pos0, int32_t slot0, float* q_out, void* stream) {
+  if (!c) return fail(BG_E_INVALID, "bg_qkv_prologue: NULL cache");
+  if (layer < 0 || layer >= c->n_layers) return fail(BG_E_INVALID, "bg_qkv_prologue: layer %d out of range", layer);
+  if (S < 1) return fail(BG_E_INVALID, "bg_qkv_prologue: S must be >= 1");
+  if (q) {
+    if (H < c->kv_heads || H % c->kv_heads) return fail(BG_E_INVALID, "heads %d must be a multiple of kv_heads %d", H, c->kv_heads);
+    if (!q_out || !q_gamma) return fail(BG_E_INVALID, "bg_qkv_prologue: q needs q_out and q_gamma");
+    if (q_stride < c->D) return fail(BG_E_INVALID, "bg_qkv_prologue: q_stride %d < head_dim %d", q_stride, c->D);
+  }
+  if (k && !k_gamma) return fail(BG_E_INVALID, "bg_qkv_prologue: k needs k_gamma");
+  const bool ropes = q || (k && !c->roll);
+  if (ropes) {
+    if (!cos_tab || !sin_tab) return fail(BG_E_INVALID, "bg_qkv_prologue: rope tables are NULL");
+    if (rot_dim < 2 || (rot_dim & 1) || rot_dim > c->D) return fail(BG_E_INVALID, "bg_qkv_prologue: bad rot_dim %d", rot_dim);
+    if (pos0 < 0 || (long)pos0 + S > rope_positions)
+      return fail(BG_E_INVALID, "bg_qkv_prologue: positions %d..%d outside the %d-row rope table", pos0, pos0 + S - 1, rope_positions);
+  }
+  if ((k || v) && (slot0 < 0 || slot0 + S > addressable(c)))
+    return fail(BG_E_INVALID, "bg_qkv_prologue: slots %d..%d beyond capacity %d", slot0, slot0 + S - 1, addressable(c));
+  bg::PrologueArgs a;
+  a.q = q;
+  a.q_stride = q_stride;
+  a.k = k;
+  a.v = v;
+  a.S = S;
+  a.H = H;
+  a.q_gamma = q_gamma;
+  a.k_gamma = k_gamma;
+  a.eps = eps;
+  a.cos_tab = cos_tab;
+  a.sin_tab = sin_tab;
+  a.rot_dim = rot_dim;
+  a.pos0 = pos0;
+  a.slot0 = slot0;
+  a.q_out = q_out;
+  hipError_t e = bg::launch_qkv_prologue(view(c, layer), a, (hipStream_t)stream);
+  return e == hipSuccess ? BG_OK : hip_fail(e, "prologue launch");
+}
+
+static int32_t ensure_workspace(bg_kv_cache* c, int S, int H) {
+  size_t counters = 0;
+  const size_t need = bg::decode_workspace_floats(view(c, 0), S, H, c->num_cus, &counters);
+  if (need <= c->ws_floats && counters <= c->ws_counters) return BG_OK;
+  if (c->ws) (void)hipFree(c->ws);
+  if (c->ws_count) (void)hipFree(c->ws_count);
+  c->ws = nullptr;
+  c->ws_count = nullptr;
+  c->ws_floats = 0;
+  c->ws_counters = 0;
+  hipError_t e = hipMalloc((void**)&c->ws, need * sizeof(float));
+  if (e == hipSuccess) e = hipMalloc((void**)&c->ws_count, counters * sizeof(unsigned));
+  if (e == hipSuccess) e = hipMemset(c->ws_count, 0, counters * sizeof(unsigned));
+  if (e != hipSuccess) {
+    if (c->ws) (void)hipFree(c->ws);
+    if (c->ws_count) (void)hipFree(c->ws_count);
+    c->ws = nullptr;
+    c->ws_count = nullptr;
+    return hip_fail(e, "attention workspace allocation");
+  }
+  c->ws_floats = need;
+  c->ws_counters = counters;
+  return BG_OK;
+}
+
+int32_t bg_attention_reserve(bg_kv_cache* c, int32_t S, int32_t H) {
+  if (!c || S < 1 || H < 1 || H % c->kv_heads) return fail(BG_E_INVALID, "bg_attention_reserve: bad arguments");
+  if (!bg::decode_supported(view(c, 0), S, H)) return BG_OK;
+  return ensure_workspace(c, S, H);
+}
+
+int32_t bg_attention(bg_kv_cache* c, int32_t layer, const float* q, int32_t S, int32_t H, int32_t pos_base, float scale,
+                     const float* gate, int32_t gate_stride, float* out, void* stream) {
+  if (!c || !q || !out) return fail(BG_E_INVALID, "bg_attention: NULL argument");
+  if (layer < 0 || layer >= c->n_layers) return fail(BG_E_INVALID, "bg_attention: layer %d out of range", layer);
+  if (S < 1 || H < 1 || H % c->kv_heads) return fail(BG_E_INVALID, "bg_attention: S %d, heads %d (kv_heads %d)", S, H, c->kv_heads);
+  if (pos_base < 0 || (long)pos_base + S > addressable(c))
+    return fail(BG_E_INVALID, "bg_attention: positions %d..%d exceed the cache (%d slots)", pos_base, pos_base + S - 1, addressable(c));
+  if (gate && gate_stride < c->D) return fail(BG_E_INVALID, "bg_attention: gate_stride %d < head_dim", gate_stride);
+  if (!(scale > 0.0f) || !std::isfinite(scale)) return fail(BG_E_INVALID, "bg_attention: scale must be positive");
+  if (c->roll) {
+    if (!c->cos_tab) return fail(BG_E_STATE, "bg_attention: sink mode needs bg_kv_set_rope first");
+    const long need = c->rope_abs ? (long)c->max_seq + c->evicted : (long)c->max_seq;
+    if (c->rope_positions < need)
+      return fail(BG_E_INVALID, "bg_attention: rope table has %d rows, read-time rotation needs %ld", c->rope_positions, need);
+  }
+  LayerView L = view(c, layer);
+  bg::AttnArgs a;
+  a.q = q;
+  a.S = S;
+  a.H = H;
+  a.pos_base = pos_base;
+  a.scale = scale;
+  a.gate = gate;
+  a.gate_stride = gate_stride;
+  a.out = out;
+  a.ws_o = nullptr;
+  a.ws_ml = nullptr;
+  a.ws_count = nullptr;
+  a.ws_floats = 0;
+  a.num_cus = c->num_cus;
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t e;
+  if (c->dtype == BG_KV_F32) {
+    e = bg::launch_attention_f32(L, a, st);
+  } else if (bg::decode_supported(L, S, H)) {
+    int32_t rc = ensure_workspace(c, S, H);
+    if (rc != BG_OK) return rc;
+    a.ws_o = c->ws;
+    a.ws_count = c->ws_count;
+    a.ws_floats = c->ws_floats;
+    e = bg::launch_attention_decode(L, a, st);
+  } else if (bg::prefill_supported(L, S, H)) {
+    e = bg::launch_attention_prefill(L, a, st);
+  } else {
+    return fail(BG_E_UNSUPPORTED, "bg_attention: no kernel for S %d, heads %d", S, H);
+  }
+  return e == hipSuccess ? BG_OK : hip_fail(e, "attention launch");
+}
+
+int32_t bg_kv_evict(bg_kv_cache* c, int32_t fill, int32_t need, int32_t* new_fill) {
+  if (!c || !new_fill) return fail(BG_E_INVALID, "bg_kv_evict: NULL argument");
+  if (!c->roll) return fail(BG_E_STATE, "bg_kv_evict: cache is not in sink mode");
+  if (fill < c->sinks || fill > c->max_seq) return fail(BG_E_INVALID, "bg_kv_evict: fill %d outside [%d, %d]", fill, c->sinks, c->max_seq);
+  int32_t nf, batch, keep;
+  int32_t rc = bg_evict_plan(fill, need, c->sinks, c->max_seq, &nf, &batch, &keep);
+  if (rc != BG_OK) return rc;
+  // rows [sinks+batch, sinks+batch+keep) become [sinks, sinks+keep): the ring origin moves by batch
+  const int W = c->max_seq - c->sinks;
+  c->head = (int)(((long)c->head + batch) % W);
+  c->evicted += batch;
+  *new_fill = nf;
+  return BG_OK;
+}
+
+int32_t bg_kv_evict_for(bg_kv_cache* c, int32_t fill, int32_t n, int32_t* new_fill) {
+  // evictFor, src/engine.ts:1214
+  if (!c || !new_fill) return fail(BG_E_INVALID, "bg_kv_evict_for: NULL argument");
+  if (c->roll && fill + n > c->max_seq) return bg_kv_evict(c, fill, fill + n - c->max_seq, new_fill);
+  *new_fill = fill;
+  return BG_OK;
+}
+
+int32_t bg_kv_region_bytes(const bg_kv_cache* c, int32_t region, int32_t count, size_t* bytes) {
+  if (!c || !bytes || count < 0) return fail(BG_E_INVALID, "bg_kv_region_bytes: bad arguments");
+  if (region == BG_K || region == BG_V) {
+    *bytes = (size_t)count * c->kv_heads * c->D * elem_bytes(c->dtype);
+  } else if ((region == BG_KSCALE || region == BG_VSCALE) && c->dtype == BG_KV_Q8) {
+    *bytes = (size_t)count * c->kv_heads * (c->D / 32) * sizeof(float);
+  } else {
+    return fail(BG_E_INVALID, "bg_kv_region_bytes: region %d not present in this storage mode", region);
+  }
+  return BG_OK;
+}
+
+static int32_t transfer(bg_kv_cache* c, int32_t layer, int32_t region, int32_t base, int32_t count, void* host,
+                        bool import_, void* stream) {
+  size_t bytes = 0;
+  int32_t rc = bg_kv_region_bytes(c, region, count, &bytes);
+  if (rc != BG_OK) return rc;
+  if (!host && count > 0) return fail(BG_E_INVALID, "snapshot transfer: NULL host buffer");
+  if (layer < 0 || layer >= c->n_layers) return fail(BG_E_INVALID, "snapshot transfer: layer %d out of range", layer);
+  if (base < 0 || base + count > addressable(c))
+    return fail(BG_E_INVALID, "snapshot transfer: positions %d..%d beyond capacity %d", base, base + count - 1, addressable(c));
+  if (count == 0) return BG_OK;
+  hipStream_t st = (hipStream_t)stream;
+  void* dev = nullptr;
+  hipError_t e = hipMalloc(&dev, bytes);
+  if (e != hipSuccess) return hip_fail(e, "snapshot staging allocation");
+  LayerView L = view(c, layer);
+  if (import_) {
+    e = hipMemcpyAsync(dev, host, bytes, hipMemcpyHostToDevice, st);
+    if (e == hipSuccess) e = bg::launch_kv_import(L, region, base, count, dev, st);
+  } else {
+    e = bg::launch_kv_export(L, region, base, count, dev, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(host, dev, bytes, hipMemcpyDeviceToHost, st);
+  }
+  if (e == hipSuccess) e = st ? hipStreamSynchronize(st) : hipDeviceSynchronize();
+  (void)hipFree(dev);
+  return e == hipSuccess ? BG_OK : hip_fail(e, import_ ? "snapshot import" : "snapshot export");
+}
+
+int32_t bg_kv_export_rows(bg_kv_cache* c, int32_t layer, int32_t region, int32_t base, int32_t count, void* host,
+                          void* stream) {
+  if (!c) return fail(BG_E_INVALID, "bg_kv_export_rows: NULL cache");
+  return transfer(c, layer, region, base, count, host, false, stream);
+}
+
+int32_t bg_kv_import_rows(bg_kv_cache* c, int32_t layer, int32_t region, int32_t base, int32_t count, const void* host,
+                          void* stream) {
+  if (!c) return fail(BG_E_INVALID, "bg_kv_import_rows: NULL cache");
+  return transfer(c, layer, region, base, count, const_cast<void*>(host), true, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,69 @@
+// Host-side launchers of the gfx950 kernels (defined in the .hip files, called by bg_api.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "bg_common.h"
+
+namespace bg {
+
+// One layer's device buffers plus the geometry the kernels need.
+struct LayerView {
+  void* k;            // K data
+  void* v;            // V data (transposed 32-slot tiles)
+  float* ks;          // q8 K scales (nullptr otherwise)
+  float* vs;          // q8 V scales
+  int cap;            // physical slots (multiple of 32)
+  int kv_heads;
+  int D;
+  int dtype;          // KvType
+  Ring ring;
+  int max_seq;
+  // read-time rotation (sink mode)
+  const float* cos_tab;
+  const float* sin_tab;
+  int rope_positions;
+  int rope_abs;       // 1: rotate by absolute position (slot + evicted for slots >= sinks)
+  int64_t evicted;    // rows dropped by eviction so far
+};
+
+// kv_pack.hip
+hipError_t launch_kv_write(const LayerView& L, int which, const float* src, int rows, int dst_row0,
+                           hipStream_t st);
+hipError_t launch_kv_export(const LayerView& L, int region, int base, int count, void* dst, hipStream_t st);
+hipError_t launch_kv_import(const LayerView& L, int region, int base, int count, const void* src, hipStream_t st);
+
+// norm_rope.hip
+struct PrologueArgs {
+  const float* q; int q_stride;
+  const float* k; const float* v;
+  int S, H;
+  const float* q_gamma; const float* k_gamma; float eps;
+  const float* cos_tab; const float* sin_tab; int rot_dim;
+  int pos0, slot0;
+  float* q_out;
+};
+hipError_t launch_qkv_prologue(const LayerView& L, const PrologueArgs& a, hipStream_t st);
+
+// attention (decode.hip, attn_f32.hip, prefill.hip)
+struct AttnArgs {
+  const float* q;
+  int S, H;
+  int pos_base;
+  float scale;
+  const float* gate; int gate_stride;
+  float* out;
+  // split-K workspace
+  float* ws_o; float* ws_ml; unsigned* ws_count; size_t ws_floats;
+  int num_cus;
+};
+hipError_t launch_attention_f32(const LayerView& L, const AttnArgs& a, hipStream_t st);
+hipError_t launch_attention_decode(const LayerView& L, const AttnArgs& a, hipStream_t st);
+hipError_t launch_attention_prefill(const LayerView& L, const AttnArgs& a, hipStream_t st);
+// workspace floats needed by the decode kernel for S rows of H heads
+size_t decode_workspace_floats(const LayerView& L, int S, int H, int num_cus, size_t* counters);
+bool decode_supported(const LayerView& L, int S, int H);
+bool prefill_supported(const LayerView& L, int S, int H);
+
+}  // namespace bg

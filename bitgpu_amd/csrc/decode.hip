@@ -1,0 +1,593 @@
+// Split-K GQA decode / verify attention over an f16 or q8 KV cache on gfx950 MFMA.
+//
+// Replaces attention_sg{,_kv16,_kv8}{,_roll}.wgsl for small S (decode S=1, speculative verify
+// S<=12): those run one subgroup per (query, head) scanning every position serially
+// (attention_sg.wgsl:31-42). Here the context is split across all CUs:
+//
+//   grid  = n_splits x KV workgroups, 4 waves each; a workgroup owns one kv head and a range of
+//           32-slot tiles; its waves take every 4th tile. All R = (H/KV)*S query rows of the
+//           GQA group are served by one read of each K/V byte.
+//   QK    = v_mfma_f32_16x16x32_f16 with K as the B operand (lane = slot, 8 dims per lane
+//           group) and a block-diagonal Q as A: row group g of the 16 output rows only sees the
+//           dims lane group g loaded, so the MFMA returns 4 partial dot products per slot that a
+//           3-shuffle reduce-scatter turns into one full score per lane -- no 12/16 padding rows.
+//           q8 codes enter the MFMA as exact f16 integers (xor/perm/pk_add, no float convert);
+//           the per-32 block scale multiplies the MFMA result. Q is split hi+lo f16 so the
+//           product keeps ~f32 accuracy.
+//   softmax = online, base 2, per 32-slot tile; probabilities (times the q8 V block scale) go
+//           through a 2 KB-per-block LDS transpose into the B operand of
+//   PV    = v_mfma_f32_16x16x32_f16 with V^T (the cache's transposed V tile, 16 B per lane)
+//           as A and P^T as B.
+//   merge = the 4 waves combine through LDS; splits write (m, l, o) partials and the last
+//           workgroup of each kv head (atomic ticket) does the log-sum-exp merge, the output
+//           gate (gate_sigmoid.wgsl:13) and the store -- one launch per layer.
+// Sink mode reads unroped K and rotates it at read by the slot's logical (or absolute) position
+// (attention_sg_roll.wgsl:40-51), in f32 before the f16 conversion.
+#include "bg_kernels.h"
+
+namespace bg {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int NW = 4;  // waves per workgroup
+constexpr float kLog2e = 1.4426950408889634f;
+
+union H8 {
+  half8 h;
+  uint4 u;
+  uint32_t w[4];
+  half2v p[4];
+};
+
+// 8 int8 codes (two little-endian words) -> 8 exact f16 values.
+__device__ inline half8 q8_to_half8(uint32_t w0, uint32_t w1) {
+  H8 r;
+  const uint32_t a0 = w0 ^ 0x80808080u, a1 = w1 ^ 0x80808080u;  // biased: u = c + 128
+  r.w[0] = __builtin_amdgcn_perm(0x64646464u, a0, 0x04010400u);   // f16 1024+u0 | 1024+u1
+  r.w[1] = __builtin_amdgcn_perm(0x64646464u, a0, 0x04030402u);
+  r.w[2] = __builtin_amdgcn_perm(0x64646464u, a1, 0x04010400u);
+  r.w[3] = __builtin_amdgcn_perm(0x64646464u, a1, 0x04030402u);
+  const half2v bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+#pragma unroll
+  for (int i = 0; i < 4; i++) r.p[i] = r.p[i] + bias;             // exact: u - 128 = c
+  return r.h;
+}
+
+__device__ inline float code_of(uint32_t w, int byte) { return (float)(int8_t)(w >> (8 * byte)); }
+
+__device__ inline uint4 ld16(const void* p) { return *(const uint4*)p; }
+
+// which dims lane group g feeds into QK MFMA #t (element e = 0..7 of the lane's half8)
+template <int D, bool QUARTER>
+__device__ inline int qk_dim(int g, int t, int e) {
+  if constexpr (QUARTER) {
+    return g * (D / 4) + 8 * t + e;
+  } else {
+    constexpr int TH = D / 64;
+    return t < TH ? g * (D / 8) + 8 * t + e : D / 2 + g * (D / 8) + 8 * (t - TH) + e;
+  }
+}
+
+struct DecodeParams {
+  LayerView L;
+  const float* q;
+  int S, H, G, R;
+  int pos_base;
+  float qscale;      // scale * log2(e) (/127 for q8 without rotation)
+  const float* gate;
+  int gate_stride;
+  float* out;
+  int n_scan;        // physical slots to scan
+  int phys_limit;    // physical slots that can hold data
+  int n_tiles, tiles_per_split, n_splits;
+  float* ws_o;       // [KV][n_splits][R][D]
+  float* ws_ml;      // [KV][n_splits][R][2]
+  unsigned* ws_count;  // [KV]
+};
+
+// Shared memory plan (bytes): Q operands, per-wave P^T tiles, per-wave corr, merge buffers.
+template <int D, int DT, bool ROLL, int NSET>
+struct DecodeSmem {
+  static constexpr bool QUARTER = (DT == KV_Q8) && !ROLL;
+  static constexpr int NT = D / 32;                       // QK MFMAs per 16-slot tile
+  static constexpr int NBV = (DT == KV_Q8) ? D / 32 : 1;  // P copies (one per V scale block)
+  static constexpr int RS = 16 * NSET;                    // padded rows
+  static constexpr int NPMAX = RS / 4;                    // QK passes
+  __host__ __device__ static size_t q_bytes(int np) { return (size_t)np * NT * 2 * 64 * 16; }
+  static constexpr size_t p_bytes_wave = (size_t)NBV * RS * 32 * 2;
+  static constexpr size_t c_bytes_wave = (size_t)RS * 4;
+  __host__ __device__ static size_t merge_bytes(int R) { return (size_t)NW * R * (D + 2) * 4; }
+  __host__ __device__ static size_t total(int np, int R) {
+    size_t a = q_bytes(np) + NW * (p_bytes_wave + c_bytes_wave);
+    size_t b = merge_bytes(R);
+    return a > b ? a : b;
+  }
+};
+
+template <int D, int DT, bool ROLL, int NSET>
+__global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
+  using SM = DecodeSmem<D, DT, ROLL, NSET>;
+  constexpr bool QUARTER = SM::QUARTER;
+  constexpr int NT = SM::NT;
+  constexpr int NBV = SM::NBV;
+  constexpr int RS = SM::RS;
+  constexpr int NB = D / 32;         // q8 scale blocks per row
+  constexpr int NSUB = QUARTER ? (D / 128) : 1;  // scale blocks inside one lane group's quarter
+  constexpr int KU = (DT == KV_Q8) ? D / 64 : D / 32;  // uint4 of K per lane per slot
+  constexpr int VU = (DT == KV_Q8) ? NB : 2 * NB;     // uint4 of V per lane per tile
+
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int g = lane >> 4;      // lane group
+  const int n = lane & 15;
+  const int kvh = blockIdx.x % p.L.kv_heads;
+  const int split = blockIdx.x / p.L.kv_heads;
+  const int NP = (p.R + 3) >> 2;
+
+  uint4* qs = (uint4*)smem;                                           // [NP][NT][2][64]
+  unsigned char* pbase = smem + SM::q_bytes(NP);
+  _Float16* pl = (_Float16*)(pbase + wave * (SM::p_bytes_wave + SM::c_bytes_wave));  // [NBV][RS][32]
+  float* cl = (float*)((unsigned char*)pl + SM::p_bytes_wave);                         // [RS]
+
+  // ---- Q operands (block diagonal, hi/lo f16) ----
+  for (int idx = tid; idx < NP * NT * 2 * 64; idx += 256) {
+    const int l = idx & 63, hl = (idx >> 6) & 1, t = (idx >> 7) % NT, pass = (idx >> 7) / NT;
+    const int gg = l >> 4, i = l & 15;
+    H8 v;
+    v.u = make_uint4(0, 0, 0, 0);
+    const int rho = 4 * pass + (i & 3);
+    if ((i >> 2) == gg && rho < p.R) {
+      const int s = rho / p.G, h = kvh * p.G + rho % p.G;
+      const float* qr = p.q + ((size_t)s * p.H + h) * D;
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const float x = qr[qk_dim<D, QUARTER>(gg, t, e)] * p.qscale;
+        const _Float16 hi = (_Float16)x;
+        v.h[e] = hl ? (_Float16)(x - (float)hi) : hi;
+      }
+    }
+    qs[idx] = v.u;
+  }
+  // zero this wave's P tiles (rows never written stay zero) and set corr = 1
+  {
+    uint4* pz = (uint4*)pl;
+    for (int i = lane; i < (int)(SM::p_bytes_wave / 16); i += 64) pz[i] = make_uint4(0, 0, 0, 0);
+    for (int i = lane; i < RS; i += 64) cl[i] = 1.0f;
+  }
+  __syncthreads();
+
+  float m[SM::NPMAX], lsum[SM::NPMAX];
+#pragma unroll
+  for (int i = 0; i < SM::NPMAX; i++) { m[i] = -1e30f; lsum[i] = 0.0f; }
+  floatx4 o[NSET][D / 16];
+#pragma unroll
+  for (int s = 0; s < NSET; s++)
+#pragma unroll
+    for (int i = 0; i < D / 16; i++) o[s][i] = floatx4{0, 0, 0, 0};
+
+  const Ring ring = p.L.ring;
+  const int cap = p.L.cap;
+  const size_t eb = (DT == KV_Q8) ? 1 : 2;
+  const unsigned char* kbase = (const unsigned char*)p.L.k + (size_t)kvh * cap * D * eb;
+  const unsigned char* vbase = (const unsigned char*)p.L.v + (size_t)kvh * cap * D * eb;
+  const float* ksb = p.L.ks + (size_t)kvh * cap * NB;
+  const float* vsb = p.L.vs + (size_t)kvh * cap * NB;
+
+  const int t_begin = split * p.tiles_per_split;
+  const int t_end = min(t_begin + p.tiles_per_split, p.n_tiles);
+
+  for (int tile = t_begin + wave; tile < t_end; tile += NW) {
+    const int j0 = tile * 32;
+    // ---------------- loads ----------------
+    uint4 kr[2][KU];
+    float ksc[2][2];
+    uint4 vr[VU];
+    float vsc[2][NB];
+#pragma unroll
+    for (int t2 = 0; t2 < 2; t2++) {
+      const int P = j0 + 16 * t2 + n;
+      const unsigned char* row = kbase + (size_t)P * D * eb;
+      if constexpr (QUARTER) {
+#pragma unroll
+        for (int i = 0; i < KU; i++) kr[t2][i] = ld16(row + g * (D / 4) + 16 * i);
+#pragma unroll
+        for (int i = 0; i < NSUB; i++) ksc[t2][i] = ksb[(size_t)P * NB + g * NSUB + i];
+      } else {
+        constexpr int HU = KU / 2;  // uint4 per half piece
+#pragma unroll
+        for (int i = 0; i < HU; i++) {
+          kr[t2][i] = ld16(row + (g * (D / 8)) * eb + 16 * i);
+          kr[t2][HU + i] = ld16(row + (D / 2 + g * (D / 8)) * eb + 16 * i);
+        }
+        if constexpr (DT == KV_Q8) {
+          ksc[t2][0] = ksb[(size_t)P * NB + (g * (D / 8)) / 32];
+          ksc[t2][1] = ksb[(size_t)P * NB + (D / 2 + g * (D / 8)) / 32];
+        }
+      }
+      if constexpr (DT == KV_Q8) {
+#pragma unroll
+        for (int b = 0; b < NB; b++) vsc[t2][b] = vsb[(size_t)P * NB + b];
+      }
+    }
+    {
+      const unsigned char* vt = vbase + ((size_t)j0 * D + (size_t)g * 8 * D) * eb;
+#pragma unroll
+      for (int b = 0; b < NB; b++) {
+        if constexpr (DT == KV_Q8) {
+          vr[b] = ld16(vt + (size_t)(32 * b + 2 * n) * 8);
+        } else {
+          vr[2 * b] = ld16(vt + (size_t)(32 * b + 2 * n) * 16);
+          vr[2 * b + 1] = ld16(vt + (size_t)(32 * b + 2 * n) * 16 + 16);
+        }
+      }
+    }
+
+    // ---------------- K operands ----------------
+    half8 kb[2][NT];
+#pragma unroll
+    for (int t2 = 0; t2 < 2; t2++) {
+      if constexpr (!ROLL) {
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+          if constexpr (DT == KV_Q8) {
+            const uint4 u = kr[t2][t >> 1];
+            kb[t2][t] = (t & 1) ? q8_to_half8(u.z, u.w) : q8_to_half8(u.x, u.y);
+          } else {
+            H8 h;  // piece 0 holds MFMAs t < NT/2, piece 1 the rest, stored back to back
+            h.u = kr[t2][t];
+            kb[t2][t] = h.h;
+          }
+        }
+      } else {
+        // read-time rotation: dims (i, i + D/2) of this lane group, at the slot's rope position
+        const int P = j0 + 16 * t2 + n;
+        int Lg = ring.logical(P);
+        Lg = P < p.phys_limit ? Lg : 0;
+        long ri = (p.L.rope_abs && Lg >= ring.sinks) ? (long)Lg + p.L.evicted : (long)Lg;
+        ri = ri < p.L.rope_positions ? ri : 0;
+        const float* ct = p.L.cos_tab + (size_t)ri * (D / 2) + g * (D / 8);
+        const float* st = p.L.sin_tab + (size_t)ri * (D / 2) + g * (D / 8);
+        constexpr int HT = NT / 2;  // MFMAs per half
+#pragma unroll
+        for (int t = 0; t < HT; t++) {
+          float a[8], b2[8];
+          if constexpr (DT == KV_Q8) {
+            const uint4 u0 = kr[t2][t >> 1], u1 = kr[t2][KU / 2 + (t >> 1)];
+            const uint32_t wa0 = (t & 1) ? u0.z : u0.x, wa1 = (t & 1) ? u0.w : u0.y;
+            const uint32_t wb0 = (t & 1) ? u1.z : u1.x, wb1 = (t & 1) ? u1.w : u1.y;
+            const float sa = ksc[t2][0] * (1.0f / 127.0f), sb = ksc[t2][1] * (1.0f / 127.0f);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+              a[e] = code_of(wa0, e) * sa;
+              a[4 + e] = code_of(wa1, e) * sa;
+              b2[e] = code_of(wb0, e) * sb;
+              b2[4 + e] = code_of(wb1, e) * sb;
+            }
+          } else {
+            H8 h0, h1;
+            h0.u = kr[t2][t];
+            h1.u = kr[t2][HT + t];
+#pragma unroll
+            for (int e = 0; e < 8; e++) { a[e] = (float)h0.h[e]; b2[e] = (float)h1.h[e]; }
+          }
+          H8 r0, r1;
+#pragma unroll
+          for (int e = 0; e < 8; e++) {
+            const float c = ct[8 * t + e], s = st[8 * t + e];
+            r0.h[e] = (_Float16)__fadd_rn(__fmul_rn(a[e], c), __fmul_rn(-b2[e], s));
+            r1.h[e] = (_Float16)__fadd_rn(__fmul_rn(b2[e], c), __fmul_rn(a[e], s));
+          }
+          kb[t2][t] = r0.h;
+          kb[t2][HT + t] = r1.h;
+        }
+      }
+    }
+
+    // ---------------- QK + online softmax, one pass per 4 query rows ----------------
+#pragma unroll
+    for (int pass = 0; pass < SM::NPMAX; pass++) {
+      if (pass >= NP) break;
+      float sc[2];
+#pragma unroll
+      for (int t2 = 0; t2 < 2; t2++) {
+        floatx4 c[NSUB];
+#pragma unroll
+        for (int i = 0; i < NSUB; i++) c[i] = floatx4{0, 0, 0, 0};
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+          H8 ahi, alo;
+          ahi.u = qs[((pass * NT + t) * 2 + 0) * 64 + lane];
+          alo.u = qs[((pass * NT + t) * 2 + 1) * 64 + lane];
+          const int sub = QUARTER ? (t >> 2) : 0;
+          c[sub] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi.h, kb[t2][t], c[sub], 0, 0, 0);
+          c[sub] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo.h, kb[t2][t], c[sub], 0, 0, 0);
+        }
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          if constexpr (QUARTER) {
+            float acc = c[0][e] * ksc[t2][0];
+#pragma unroll
+            for (int i = 1; i < NSUB; i++) acc = fmaf(c[i][e], ksc[t2][i], acc);
+            v[e] = acc;
+          } else {
+            v[e] = c[0][e];
+          }
+        }
+        // reduce-scatter over the 4 lane groups: lane group g ends with query row g of the pass
+        const bool lowg = g < 2;
+        const float s0 = __shfl_xor(lowg ? v[2] : v[0], 32, 64);
+        const float s1 = __shfl_xor(lowg ? v[3] : v[1], 32, 64);
+        const float k0 = (lowg ? v[0] : v[2]) + s0;
+        const float k1 = (lowg ? v[1] : v[3]) + s1;
+        const bool odd = g & 1;
+        const float s2 = __shfl_xor(odd ? k0 : k1, 16, 64);
+        sc[t2] = (odd ? k1 : k0) + s2;
+      }
+      // mask + online softmax for row rho = 4*pass + g
+      const int rho = 4 * pass + g;
+      const int qi = rho / p.G;
+      const bool row_ok = rho < p.R;
+      const int limit = p.pos_base + qi;
+      float x[2];
+#pragma unroll
+      for (int t2 = 0; t2 < 2; t2++) {
+        const int P = j0 + 16 * t2 + n;
+        const int Lg = ring.logical(P);
+        const bool ok = row_ok && P < p.n_scan && P < p.phys_limit && Lg <= limit;
+        x[t2] = ok ? sc[t2] : -INFINITY;
+      }
+      const float mt = group16_max(fmaxf(x[0], x[1]));
+      const float mn = fmaxf(m[pass], mt);
+      const float corr = exp2f(m[pass] - mn);
+      const float p0 = exp2f(x[0] - mn), p1 = exp2f(x[1] - mn);
+      lsum[pass] = lsum[pass] * corr + p0 + p1;
+      m[pass] = mn;
+      if (n == 0 && rho < RS) cl[rho] = corr;
+      if (rho < RS) {
+#pragma unroll
+        for (int t2 = 0; t2 < 2; t2++) {
+          const int j = 16 * t2 + n;
+          const float pv = t2 ? p1 : p0;
+          const int col = tile_panel(j) * 8 + tile_index(j);
+#pragma unroll
+          for (int b = 0; b < NBV; b++) {
+            const float w = (DT == KV_Q8) ? pv * (vsc[t2][b] * (1.0f / 127.0f)) : pv;
+            pl[((size_t)b * RS + rho) * 32 + col] = (_Float16)w;
+          }
+        }
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // ---------------- PV ----------------
+    half8 va[NB][2];
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+      if constexpr (DT == KV_Q8) {
+        va[b][0] = q8_to_half8(vr[b].x, vr[b].y);
+        va[b][1] = q8_to_half8(vr[b].z, vr[b].w);
+      } else {
+        H8 e0, e1;
+        e0.u = vr[2 * b];
+        e1.u = vr[2 * b + 1];
+        va[b][0] = e0.h;
+        va[b][1] = e1.h;
+      }
+    }
+#pragma unroll
+    for (int st = 0; st < NSET; st++) {
+      const float cr = cl[16 * st + n];
+#pragma unroll
+      for (int i = 0; i < D / 16; i++) o[st][i] *= cr;
+#pragma unroll
+      for (int b = 0; b < NB; b++) {
+        H8 pb;
+        pb.u = *(const uint4*)(pl + ((size_t)(NBV > 1 ? b : 0) * RS + 16 * st + n) * 32 + 8 * g);
+        o[st][2 * b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[b][0], pb.h, o[st][2 * b], 0, 0, 0);
+        o[st][2 * b + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[b][1], pb.h, o[st][2 * b + 1], 0, 0, 0);
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+
+  // ---------------- combine the 4 waves of the workgroup ----------------
+  __syncthreads();
+  float* mw = (float*)smem;               // [NW][R]
+  float* lw = mw + NW * p.R;              // [NW][R]
+  float* ow = lw + NW * p.R;              // [NW][R][D]
+#pragma unroll
+  for (int pass = 0; pass < SM::NPMAX; pass++) {
+    if (pass >= NP) break;
+    const float lt = group16_sum(lsum[pass]);
+    const int rho = 4 * pass + g;
+    if (n == 0 && rho < p.R) {
+      mw[wave * p.R + rho] = m[pass];
+      lw[wave * p.R + rho] = lt;
+    }
+  }
+#pragma unroll
+  for (int st = 0; st < NSET; st++) {
+    const int rho = 16 * st + n;
+    if (rho < p.R) {
+#pragma unroll
+      for (int b = 0; b < NB; b++)
+#pragma unroll
+        for (int par = 0; par < 2; par++)
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const int d = 32 * b + 2 * (4 * g + e) + par;
+            ow[((size_t)wave * p.R + rho) * D + d] = o[st][2 * b + par][e];
+          }
+    }
+  }
+  __syncthreads();
+
+  const bool single = p.n_splits == 1;
+  float* wso = p.ws_o + ((size_t)kvh * p.n_splits + split) * p.R * D;
+  float* wsml = p.ws_ml + ((size_t)kvh * p.n_splits + split) * p.R * 2;
+  for (int idx = tid; idx < p.R * D; idx += 256) {
+    const int rho = idx / D, d = idx % D;
+    float M = -1e30f;
+#pragma unroll
+    for (int w = 0; w < NW; w++) M = fmaxf(M, mw[w * p.R + rho]);
+    float acc = 0.0f, lt = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; w++) {
+      const float f = exp2f(mw[w * p.R + rho] - M);
+      acc += ow[((size_t)w * p.R + rho) * D + d] * f;
+      lt += lw[w * p.R + rho] * f;
+    }
+    if (single) {
+      const int s = rho / p.G, h = kvh * p.G + rho % p.G;
+      float r = acc / lt;
+      if (p.gate) r = r / (1.0f + expf(-p.gate[((size_t)s * p.H + h) * p.gate_stride + d]));
+      p.out[((size_t)s * p.H + h) * D + d] = r;
+    } else {
+      wso[idx] = acc;
+      if (d == 0) {
+        wsml[2 * rho] = M;
+        wsml[2 * rho + 1] = lt;
+      }
+    }
+  }
+  if (single) return;
+
+  // ---------------- last workgroup of this kv head merges the splits ----------------
+  __shared__ unsigned s_last;
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned prev = atomicAdd(&p.ws_count[kvh], 1u);
+    s_last = (prev == (unsigned)(p.n_splits - 1)) ? 1u : 0u;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+  const float* wo = p.ws_o + (size_t)kvh * p.n_splits * p.R * D;
+  const float* wml = p.ws_ml + (size_t)kvh * p.n_splits * p.R * 2;
+  for (int idx = tid; idx < p.R * D; idx += 256) {
+    const int rho = idx / D, d = idx % D;
+    float M = -1e30f;
+    for (int sp = 0; sp < p.n_splits; sp++) M = fmaxf(M, __builtin_nontemporal_load(&wml[((size_t)sp * p.R + rho) * 2]));
+    float acc = 0.0f, lt = 0.0f;
+    for (int sp = 0; sp < p.n_splits; sp++) {
+      const float f = exp2f(__builtin_nontemporal_load(&wml[((size_t)sp * p.R + rho) * 2]) - M);
+      acc += __builtin_nontemporal_load(&wo[((size_t)sp * p.R + rho) * D + d]) * f;
+      lt += __builtin_nontemporal_load(&wml[((size_t)sp * p.R + rho) * 2 + 1]) * f;
+    }
+    const int s = rho / p.G, h = kvh * p.G + rho % p.G;
+    float r = acc / lt;
+    if (p.gate) r = r / (1.0f + expf(-p.gate[((size_t)s * p.H + h) * p.gate_stride + d]));
+    p.out[((size_t)s * p.H + h) * D + d] = r;
+  }
+  if (tid == 0) p.ws_count[kvh] = 0u;  // ready for the next launch
+}
+
+// ------------------------------------------------------------------------------------------
+static int nset_for(int R) { return (R + 15) / 16; }
+
+bool decode_supported(const LayerView& L, int S, int H) {
+  if (L.dtype == KV_F32) return false;
+  if (L.D != 128 && L.D != 256) return false;
+  const int G = H / L.kv_heads;
+  const int R = G * S;
+  return R >= 1 && nset_for(R) <= 3;
+}
+
+struct Split { int n_tiles, tps, n_splits, n_scan, phys_limit; };
+
+static Split plan_split(const LayerView& L, int S, int pos_base, int num_cus) {
+  Split s;
+  if (L.ring.roll && L.ring.head != 0) {
+    s.n_scan = L.max_seq;
+  } else {
+    s.n_scan = pos_base + S;
+  }
+  s.phys_limit = L.ring.roll ? L.max_seq : L.cap;
+  s.n_tiles = (s.n_scan + 31) / 32;
+  const int target = 2 * (num_cus > 0 ? num_cus : 256);  // workgroups
+  int tps = (s.n_tiles * L.kv_heads + target - 1) / target;
+  tps = tps < NW ? NW : tps;
+  s.tps = tps;
+  s.n_splits = (s.n_tiles + tps - 1) / tps;
+  return s;
+}
+
+size_t decode_workspace_floats(const LayerView& L, int S, int H, int num_cus, size_t* counters) {
+  // upper bound over every pos_base: tiles_per_split >= NW, so at most cap/32/NW splits
+  (void)num_cus;
+  const int R = (H / L.kv_heads) * S;
+  const int ns_max = (L.cap / 32 + NW - 1) / NW;
+  *counters = (size_t)L.kv_heads;
+  return (size_t)L.kv_heads * ns_max * R * ((size_t)L.D + 2);
+}
+
+template <int D, int DT, bool ROLL, int NSET>
+static hipError_t launch_cfg(const LayerView& L, const AttnArgs& a, const Split& sp, hipStream_t st) {
+  using SM = DecodeSmem<D, DT, ROLL, NSET>;
+  DecodeParams p;
+  p.L = L;
+  p.q = a.q;
+  p.S = a.S;
+  p.H = a.H;
+  p.G = a.H / L.kv_heads;
+  p.R = p.G * a.S;
+  p.pos_base = a.pos_base;
+  p.qscale = a.scale * kLog2e * (SM::QUARTER ? (1.0f / 127.0f) : 1.0f);
+  p.gate = a.gate;
+  p.gate_stride = a.gate_stride;
+  p.out = a.out;
+  p.n_scan = sp.n_scan;
+  p.phys_limit = sp.phys_limit;
+  p.n_tiles = sp.n_tiles;
+  p.tiles_per_split = sp.tps;
+  p.n_splits = sp.n_splits;
+  p.ws_o = a.ws_o;
+  p.ws_ml = a.ws_o ? a.ws_o + (size_t)L.kv_heads * sp.n_splits * p.R * D : nullptr;
+  p.ws_count = a.ws_count;
+  const int NP = (p.R + 3) / 4;
+  const size_t smem = SM::total(NP, p.R);
+  if (smem > 160 * 1024) return hipErrorInvalidValue;
+  (void)hipFuncSetAttribute((const void*)decode_kernel<D, DT, ROLL, NSET>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+  hipLaunchKernelGGL((decode_kernel<D, DT, ROLL, NSET>), dim3(sp.n_splits * L.kv_heads), dim3(256), smem, st, p);
+  return hipGetLastError();
+}
+
+template <int D, int DT, bool ROLL>
+static hipError_t launch_nset(const LayerView& L, const AttnArgs& a, const Split& sp, int nset, hipStream_t st) {
+  switch (nset) {
+    case 1: return launch_cfg<D, DT, ROLL, 1>(L, a, sp, st);
+    case 2: return launch_cfg<D, DT, ROLL, 2>(L, a, sp, st);
+    default: return launch_cfg<D, DT, ROLL, 3>(L, a, sp, st);
+  }
+}
+
+template <int D>
+static hipError_t launch_d(const LayerView& L, const AttnArgs& a, const Split& sp, int nset, hipStream_t st) {
+  const bool roll = L.ring.roll != 0;
+  if (L.dtype == KV_Q8) {
+    return roll ? launch_nset<D, KV_Q8, true>(L, a, sp, nset, st) : launch_nset<D, KV_Q8, false>(L, a, sp, nset, st);
+  }
+  return roll ? launch_nset<D, KV_F16, true>(L, a, sp, nset, st) : launch_nset<D, KV_F16, false>(L, a, sp, nset, st);
+}
+
+hipError_t launch_attention_decode(const LayerView& L, const AttnArgs& a, hipStream_t st) {
+  Split sp = plan_split(L, a.S, a.pos_base, a.num_cus);
+  const int R = (a.H / L.kv_heads) * a.S;
+  // the split partials must fit the workspace the host sized
+  const size_t need = (size_t)L.kv_heads * sp.n_splits * R * ((size_t)L.D + 2);
+  if (sp.n_splits > 1 && (a.ws_o == nullptr || need > a.ws_floats)) return hipErrorInvalidValue;
+  const int nset = nset_for(R);
+  return L.D == 128 ? launch_d<128>(L, a, sp, nset, st) : launch_d<256>(L, a, sp, nset, st);
+}
+
+}  // namespace bg

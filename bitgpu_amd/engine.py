@@ -1,0 +1,264 @@
+"""Host-side mirror of the reference engine's per-layer attention dispatch, over the C ABI.
+
+The reference (stfurkan/bitgpu v0.19.1, src/engine.ts) records, per layer:
+
+* ``appendKV(pass, src, which, li, rows, dstRow0)``            -> :meth:`KvCache.append_kv`
+* ``attIns(qr, li)`` + ``runN(ATT, [S,H,KV,D,posBase,Ltot])``  -> :func:`attention`
+* the fused decode branch of ``layer()`` (1519-1547) and its prefill branch (1562-1581)
+                                                               -> :func:`layer_attention`
+* the full-attention branch of ``hybridLayer()`` (1465-1493)   -> :func:`hybrid_full_attention`
+* ``ensureKvCapacity`` / ``evict`` / ``evictFor`` / ``saveCache`` / ``restoreCache``
+                                                               -> :class:`KvCache` methods
+* ``synthRope`` (117-147)                                      -> :func:`rope_tables`
+
+Device memory is owned by torch tensors (``cuda`` device, float32, contiguous); only raw
+pointers cross the boundary. Every call is enqueued on torch's current stream. There is no CPU
+fallback: without the built HIP library these functions raise.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+
+import numpy as np
+
+from ._lib import (BG_K, BG_KSCALE, BG_ROPE_ABSOLUTE, BG_ROPE_SLOT, BG_V, BG_VSCALE, KV_DTYPES, check,
+                   lib)
+
+__all__ = ["KvCache", "attention", "qkv_prologue", "layer_attention", "hybrid_full_attention",
+           "rope_tables", "evict_plan"]
+
+
+def _stream():
+    import torch
+    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _ptr(t):
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise ValueError("bitgpu_amd: expected a device (cuda) tensor")
+    if not t.is_contiguous():
+        raise ValueError("bitgpu_amd: expected a contiguous tensor")
+    return C.c_void_p(t.data_ptr())
+
+
+def _f32(t, name):
+    import torch
+    if t.dtype != torch.float32:
+        raise TypeError(f"bitgpu_amd: {name} must be float32, got {t.dtype}")
+    return t
+
+
+def rope_tables(theta: float, rot_dim: int, positions: int, yarn: dict | None = None):
+    """synthRope (src/engine.ts:117-147): f32 ``[positions, rot_dim/2]`` cos/sin host arrays."""
+    half = rot_dim // 2
+    cos = np.empty((positions, half), np.float32)
+    sin = np.empty((positions, half), np.float32)
+    factor = float(yarn["factor"]) if yarn else 1.0
+    orig = int(yarn["original_max_position_embeddings"]) if yarn else 0
+    check(lib().bg_rope_tables(float(theta), int(rot_dim), int(positions), factor, orig,
+                               cos.ctypes.data_as(C.c_void_p), sin.ctypes.data_as(C.c_void_p)))
+    return cos, sin
+
+
+def evict_plan(fill: int, need: int, sinks: int, max_seq_len: int):
+    """evict() arithmetic of src/engine.ts:1188-1212 -> (new_fill, batch, keep)."""
+    nf, b, k = C.c_int32(), C.c_int32(), C.c_int32()
+    check(lib().bg_evict_plan(fill, need, sinks, max_seq_len, C.byref(nf), C.byref(b), C.byref(k)))
+    return nf.value, b.value, k.value
+
+
+class KvCache:
+    """The engine's per-layer KV cache (Kc/Vc/Ksc/Vsc, src/engine.ts:1044-1079).
+
+    ``kv_cache`` is EngineOptions.kvCache ('f32' | 'f16' | 'q8'), ``overflow`` 'error' | 'sinks'
+    and ``sink_tokens`` EngineOptions.sinkTokens (src/types.ts:138-177). ``rope_positions``
+    selects the sink-mode key rotation: 'slot' (the reference's cache-relative positions) or
+    'absolute' (true token positions).
+    """
+
+    def __init__(self, n_layers: int, kv_heads: int, head_dim: int, kv_cache: str = "f32",
+                 max_seq_len: int = 2048, capacity: int | None = None, overflow: str = "error",
+                 sink_tokens: int = 4, rope_positions: str = "slot"):
+        if kv_cache not in KV_DTYPES:
+            raise ValueError(f"bitgpu_amd: kvCache must be one of {sorted(KV_DTYPES)}")
+        if overflow not in ("error", "sinks"):
+            raise ValueError("bitgpu_amd: overflow must be 'error' or 'sinks'")
+        self.n_layers, self.kv_heads, self.head_dim = n_layers, kv_heads, head_dim
+        self.kv_cache, self.max_seq_len = kv_cache, max_seq_len
+        self.roll = overflow == "sinks"
+        self.sinks = max(1, int(sink_tokens)) if self.roll else 0
+        self._h = C.c_void_p()
+        mode = BG_ROPE_ABSOLUTE if rope_positions == "absolute" else BG_ROPE_SLOT
+        check(lib().bg_kv_create(n_layers, kv_heads, head_dim, KV_DTYPES[kv_cache],
+                                 0 if capacity is None else int(capacity), max_seq_len,
+                                 1 if self.roll else 0, self.sinks, mode, C.byref(self._h)))
+        self._rope_keepalive = None
+
+    # -- lifecycle ---------------------------------------------------------------------------
+    def close(self):
+        if self._h:
+            lib().bg_kv_destroy(self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def handle(self):
+        return self._h
+
+    @property
+    def capacity(self) -> int:
+        c = C.c_int32()
+        check(lib().bg_kv_capacity(self._h, C.byref(c)))
+        return c.value
+
+    def ensure_capacity(self, needed: int):
+        """ensureKvCapacity (src/engine.ts:1120-1178); raises GpuOutOfMemoryError on failure
+        with the old buffers kept."""
+        check(lib().bg_kv_grow(self._h, int(needed), _stream()))
+
+    def set_rope(self, cos_dev, sin_dev):
+        """Bind the sink-mode rotation tables (rollCosT/rollSinT, src/engine.ts:1097-1104)."""
+        _f32(cos_dev, "cos")
+        _f32(sin_dev, "sin")
+        check(lib().bg_kv_set_rope(self._h, _ptr(cos_dev), _ptr(sin_dev), cos_dev.shape[0], 2 * cos_dev.shape[1]))
+        self._rope_keepalive = (cos_dev, sin_dev)
+
+    # -- writes ------------------------------------------------------------------------------
+    def append_kv(self, src, which: int, li: int, rows: int, dst_row0: int):
+        """appendKV (src/engine.ts:1385-1393): ``rows`` f32 rows at reference row ``dst_row0``."""
+        _f32(src, "src")
+        if src.numel() < rows * self.head_dim:
+            raise ValueError("bitgpu_amd: append_kv source is smaller than rows * head_dim")
+        check(lib().bg_kv_write(self._h, li, which, _ptr(src), int(rows), int(dst_row0), _stream()))
+
+    # -- sink-mode eviction ------------------------------------------------------------------
+    def evict(self, fill: int, need: int) -> int:
+        nf = C.c_int32()
+        check(lib().bg_kv_evict(self._h, int(fill), int(need), C.byref(nf)))
+        return nf.value
+
+    def evict_for(self, fill: int, n: int) -> int:
+        nf = C.c_int32()
+        check(lib().bg_kv_evict_for(self._h, int(fill), int(n), C.byref(nf)))
+        return nf.value
+
+    # -- snapshot byte format ----------------------------------------------------------------
+    def region_bytes(self, region: int, count: int) -> int:
+        b = C.c_size_t()
+        check(lib().bg_kv_region_bytes(self._h, region, count, C.byref(b)))
+        return b.value
+
+    def export_rows(self, li: int, region: int, base: int, count: int) -> bytes:
+        buf = C.create_string_buffer(max(1, self.region_bytes(region, count)))
+        check(lib().bg_kv_export_rows(self._h, li, region, base, count, C.cast(buf, C.c_void_p), _stream()))
+        return buf.raw[: self.region_bytes(region, count)]
+
+    def import_rows(self, li: int, region: int, base: int, count: int, data: bytes):
+        if len(data) != self.region_bytes(region, count):
+            raise ValueError("bitgpu_amd: import size does not match the region")
+        buf = C.create_string_buffer(bytes(data), max(1, len(data)))
+        check(lib().bg_kv_import_rows(self._h, li, region, base, count, C.cast(buf, C.c_void_p), _stream()))
+
+    def _regions(self):
+        return [BG_K, BG_V, BG_KSCALE, BG_VSCALE] if self.kv_cache == "q8" else [BG_K, BG_V]
+
+    def save_snapshot(self, length: int, base: int = 0) -> bytes:
+        """KV part of saveCache (src/engine.ts:2736-2805): per layer K, V (then Ksc, Vsc under
+        q8) for positions [base, length), in the reference byte layout."""
+        count = length - base
+        return b"".join(self.export_rows(li, r, base, count) for li in range(self.n_layers) for r in self._regions())
+
+    def restore_snapshot(self, data: bytes, length: int, base: int = 0):
+        """KV part of restoreCache (src/engine.ts:2807-2872)."""
+        count = length - base
+        expect = self.n_layers * sum(self.region_bytes(r, count) for r in self._regions())
+        if len(data) != expect:
+            raise ValueError(f"restoreCache: snapshot data is {len(data)} bytes, expected {expect}")
+        self.ensure_capacity(length)
+        off = 0
+        for li in range(self.n_layers):
+            for r in self._regions():
+                n = self.region_bytes(r, count)
+                self.import_rows(li, r, base, count, data[off: off + n])
+                off += n
+
+
+def attention(cache: KvCache, li: int, qr, S: int, H: int, pos_base: int, scale: float | None = None,
+              gate=None, gate_stride: int | None = None, out=None):
+    """runN(ATT, [S,H,KV,D,posBase,Ltot], attIns(qr, li), att, S*H) (src/engine.ts:1543,1579-1580);
+    with ``gate`` the hybrid's attention_online_cache + gate_sigmoid (1486-1491)."""
+    import torch
+    D = cache.head_dim
+    _f32(qr, "q")
+    if qr.numel() != S * H * D:
+        raise ValueError("bitgpu_amd: q must hold S*H*head_dim values")
+    if out is None:
+        out = torch.empty((S, H, D), dtype=torch.float32, device=qr.device)
+    if scale is None:
+        scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))  # attention_sg.wgsl:24
+    gs = 0
+    if gate is not None:
+        _f32(gate, "gate")
+        gs = int(gate_stride if gate_stride is not None else D)
+    check(lib().bg_attention(cache.handle, li, _ptr(qr), S, H, int(pos_base), float(scale), _ptr(gate), gs,
+                             _ptr(out), _stream()))
+    return out
+
+
+def qkv_prologue(cache: KvCache, li: int, q, k, v, S: int, H: int, q_gamma, k_gamma, eps: float,
+                 cos_tab, sin_tab, rot_dim: int, pos0: int, slot0: int, q_stride: int | None = None,
+                 q_out=None):
+    """Fused q/k RMSNorm + RoPE + K/V cache write (see include/bitgpu_attn.h bg_qkv_prologue)."""
+    import torch
+    D = cache.head_dim
+    if q is not None and q_out is None:
+        q_out = torch.empty((S, H, D), dtype=torch.float32, device=q.device)
+    for t, nm in ((q, "q"), (k, "k"), (v, "v"), (q_gamma, "q_gamma"), (k_gamma, "k_gamma")):
+        if t is not None:
+            _f32(t, nm)
+    check(lib().bg_qkv_prologue(cache.handle, li, _ptr(q), int(q_stride or D), _ptr(k), _ptr(v), S, H,
+                                _ptr(q_gamma), _ptr(k_gamma), float(eps), _ptr(cos_tab), _ptr(sin_tab),
+                                int(cos_tab.shape[0]) if cos_tab is not None else 0, int(rot_dim), int(pos0),
+                                int(slot0), _ptr(q_out), _stream()))
+    return q_out
+
+
+def layer_attention(cache: KvCache, li: int, q, k, v, S: int, H: int, pos_base: int, q_norm, k_norm,
+                    eps: float, cos_tab, sin_tab, slot: int | None = None):
+    """The attention block of the dense ``layer()`` (src/engine.ts:1519-1547 decode, 1562-1581
+    prefill/verify): q/k norm + rope, K/V append at ``posBase`` (the cache slot), attention.
+
+    q: [S, H, D], k/v: [S, KV, D] projections (f32, device). RoPE uses position ``pos_base + s``
+    for the query and the key (the engine's posBase is the slot, src/engine.ts:994-1009,
+    1782-1798); in sink mode keys are stored unroped. Returns att [S, H, D].
+    """
+    slot = pos_base if slot is None else slot
+    qr = qkv_prologue(cache, li, q, k, v, S, H, q_norm, k_norm, eps, cos_tab, sin_tab,
+                      cache.head_dim, pos_base, slot)
+    return attention(cache, li, qr, S, H, slot)
+
+
+def hybrid_full_attention(cache: KvCache, li: int, qg, k, v, S: int, H: int, pos_base: int, q_norm, k_norm,
+                          eps: float, cos_tab, sin_tab, rot_dim: int):
+    """Full-attention branch of ``hybridLayer()`` (src/engine.ts:1465-1493) after the
+    projections: split_head (query | gate interleave of the doubled q_proj), q/k RMSNorm with
+    the baked (1 + weight) scale, partial RoPE, K/V append, attention_online_cache{,_kv8} with
+    scale 1/sqrt(head_dim), then gate_sigmoid. qg: [S, H, 2D]; returns gated [S, H, D]."""
+    D = cache.head_dim
+    qr = qkv_prologue(cache, li, qg, k, v, S, H, q_norm, k_norm, eps, cos_tab, sin_tab, rot_dim, pos_base,
+                      pos_base, q_stride=2 * D)
+    import torch
+    scale = float(np.float32(1.0 / math.sqrt(D)))  # the hybrid's ['f', 1/Math.sqrt(Dh)] param
+    out = torch.empty((S, H, D), dtype=torch.float32, device=qg.device)
+    # the gate half of each [2D] row starts D floats in; its row stride is 2D
+    check(lib().bg_attention(cache.handle, li, _ptr(qr), S, H, int(pos_base), scale,
+                             C.c_void_p(qg.data_ptr() + D * 4), 2 * D, _ptr(out), _stream()))
+    return out

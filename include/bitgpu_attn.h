@@ -1,0 +1,163 @@
+/* bitgpu_attn.h -- C ABI of the MI355X (gfx950) attention hot path.
+ *
+ * Drop-in replacement for the per-layer attention dispatch of bitgpu v0.19.1's WebGPU engine
+ * (src/engine.ts). Every entry point names the reference interface it replaces (file:line,
+ * relative to the reference repository root).
+ *
+ * Conventions
+ *   - All functions return int32_t status: BG_OK (0) or a negative BG_E_* code; the message of
+ *     the last failure on the calling thread is in bg_last_error_message(). Nothing throws.
+ *   - Device buffers are plain device pointers (hipMalloc'd or torch-owned); host buffers are
+ *     plain host pointers. No framework types cross this boundary.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the default stream). Work is enqueued
+ *     in order on that stream; calls return before the GPU finishes unless stated otherwise.
+ *   - A cache object is not re-entrant: calls on one cache must be serialized by the caller
+ *     (the reference serializes every engine op through one promise chain, src/engine.ts:2877-2887).
+ *   - Kernels never allocate. Host-side allocations happen only in bg_kv_create, bg_kv_grow and
+ *     bg_attention_reserve (or lazily, once, on the first bg_attention that needs more workspace).
+ *
+ * Storage modes mirror EngineOptions.kvCache (src/types.ts:143-154): f32, f16 (one RNE rounding
+ * at write, shaders/copy_kv16.wgsl:13) and q8 (int8 codes + one f32 scale per 32 values,
+ * shaders/copy_kv8.wgsl:24-40). The device layout is private (head-major, V stored in
+ * 32-position transposed tiles); bg_kv_export_rows / bg_kv_import_rows convert to and from the
+ * reference's snapshot byte layout (src/engine.ts:2724-2734).
+ */
+#ifndef BITGPU_ATTN_H
+#define BITGPU_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BG_OK 0
+#define BG_E_INVALID (-1)     /* bad argument */
+#define BG_E_OOM (-2)         /* device allocation failed (the reference's GpuOutOfMemoryError) */
+#define BG_E_DEVICE (-3)      /* HIP runtime error */
+#define BG_E_UNSUPPORTED (-4) /* shape or mode this build does not implement */
+#define BG_E_STATE (-5)       /* not valid in the cache's current state */
+
+enum { BG_KV_F32 = 0, BG_KV_F16 = 1, BG_KV_Q8 = 2 };
+enum { BG_K = 0, BG_V = 1, BG_KSCALE = 2, BG_VSCALE = 3 };
+enum { BG_ROPE_SLOT = 0, BG_ROPE_ABSOLUTE = 1 };
+
+typedef struct bg_kv_cache bg_kv_cache;
+
+/* ---- utilities ------------------------------------------------------------------------- */
+
+/* Last failure message on this thread ("" if none). Replaces the Error('bitgpu: ...') text of
+ * src/errors.ts:14-19. */
+const char* bg_last_error_message(void);
+
+/* Library version string. */
+const char* bg_version(void);
+
+/* RoPE tables f32 [positions, rot_dim/2]: f64 angles p * theta^(-2j/rot_dim), each entry
+ * rounded once to f32; YaRN when yarn_factor > 1 (beta_fast 32, beta_slow 1, mscale
+ * 0.1 ln(factor) + 1). Host-only. Replaces synthRope, src/engine.ts:117-147. */
+int32_t bg_rope_tables(double theta, int32_t rot_dim, int32_t positions, double yarn_factor,
+                       int32_t yarn_original_max_positions, float* cos_out, float* sin_out);
+
+/* Sink-mode eviction arithmetic (host-only, no cache): evict(fill, need) of
+ * src/engine.ts:1188-1212. Outputs the new fill, the dropped batch and the kept count. */
+int32_t bg_evict_plan(int32_t fill, int32_t need, int32_t sinks, int32_t max_seq_len,
+                      int32_t* new_fill, int32_t* batch, int32_t* keep);
+
+/* Synchronize a stream (NULL = device). */
+int32_t bg_stream_sync(void* stream);
+
+/* ---- KV cache lifecycle ------------------------------------------------------------------
+ * Replaces the Kc/Vc/Ksc/Vsc allocation of src/engine.ts:1044-1079, the kvCache/overflow/
+ * sinkTokens/maxSeqLen options (src/types.ts:138-177) and the roll statics (1094-1111). */
+int32_t bg_kv_create(int32_t n_layers, int32_t kv_heads, int32_t head_dim, int32_t dtype,
+                     int32_t capacity, int32_t max_seq_len, int32_t roll, int32_t sinks,
+                     int32_t rope_pos_mode, bg_kv_cache** out);
+int32_t bg_kv_destroy(bg_kv_cache* cache);
+
+/* Current capacity in positions. */
+int32_t bg_kv_capacity(const bg_kv_cache* cache, int32_t* capacity);
+
+/* ensureKvCapacity, src/engine.ts:1120-1178: grow every layer to >= min(needed, max_seq_len)
+ * positions (doubling), preserving content. On allocation failure the cache keeps its old
+ * buffers and BG_E_OOM is returned (the reference's rollback, 1157-1173). Synchronous. */
+int32_t bg_kv_grow(bg_kv_cache* cache, int32_t needed, void* stream);
+
+/* Device rope tables [positions, rot_dim/2] used for the sink-mode read-time K rotation
+ * (the rollCosT/rollSinT bindings of attIns, src/engine.ts:1097-1104,1395-1399). The caller
+ * owns the buffers; they must cover max_seq_len positions (slot mode) or every absolute
+ * position attended (absolute mode). */
+int32_t bg_kv_set_rope(bg_kv_cache* cache, const float* cos_tab, const float* sin_tab,
+                       int32_t positions, int32_t rot_dim);
+
+/* ---- KV writes ---------------------------------------------------------------------------- */
+
+/* appendKV, src/engine.ts:1385-1393 (copy.wgsl / copy_kv16.wgsl / copy_kv8.wgsl): `rows` f32
+ * rows of head_dim values, row r landing at reference cache row dst_row0 + r, i.e. logical
+ * position (dst_row0 + r) / kv_heads and kv head (dst_row0 + r) % kv_heads. which = BG_K|BG_V. */
+int32_t bg_kv_write(bg_kv_cache* cache, int32_t layer, int32_t which, const float* src,
+                    int32_t rows, int32_t dst_row0, void* stream);
+
+/* Fused attention prologue for S positions in one launch, replacing (src/engine.ts)
+ *   decode : rmsnorm_rope_sg(Q) + ROPE_K / rmsnorm_rope_sg_kv8(K into the cache) + appendKV(V)
+ *            (1527-1540; shaders/rmsnorm_rope_sg*.wgsl)
+ *   prefill: rms(q), rms(k), rope(q), rope(k), appendKV(K), appendKV(V) (1569-1576)
+ *   hybrid : split_head(query) + rms + rope_partial (q and k) + appendKV(K, V) (1470-1485)
+ * q: [S, H, q_stride] (first head_dim values of each row are the query; q_stride = 2*head_dim
+ * reads the hybrid's interleaved query|gate projection), k, v: [S, KV, head_dim]. Any of q, k,
+ * v may be NULL to skip that part. Q rows are RMSNormed with q_gamma, roped at pos0 + s and
+ * written to q_out [S, H, head_dim]; K rows are normed with k_gamma, roped at pos0 + s (left
+ * unroped in a sink-mode cache, which rotates at read) and stored at logical slot slot0 + s;
+ * V rows are stored unchanged at slot0 + s. Tables cos_tab/sin_tab: [rope_positions,
+ * rot_dim/2] (the engine's cos/sin caches, indexed by position instead of the per-call [S, D]
+ * expansion of ropeBufs, src/engine.ts:994-1009); rot_dim <= head_dim (dims >= rot_dim pass
+ * through). */
+int32_t bg_qkv_prologue(bg_kv_cache* cache, int32_t layer, const float* q, int32_t q_stride,
+                        const float* k, const float* v, int32_t S, int32_t H,
+                        const float* q_gamma, const float* k_gamma, float eps,
+                        const float* cos_tab, const float* sin_tab, int32_t rope_positions,
+                        int32_t rot_dim, int32_t pos0, int32_t slot0, float* q_out, void* stream);
+
+/* ---- attention ---------------------------------------------------------------------------
+ * runN(ATT, [S,H,KV,D,posBase,Ltot], attIns(qr, li), att, S*H), src/engine.ts:1543,1579-1580
+ * (attention_{sg,wg}{,_kv16,_kv8}{,_roll}.wgsl) and the hybrid
+ * attention_online_cache{,_kv8} + gate_sigmoid, src/engine.ts:1486-1491.
+ * q: [S, H, head_dim] f32 (already normed/roped); query s sits at logical slot pos_base + s and
+ * attends every resident slot <= pos_base + s. scale: the softmax scale (the dense kernels use
+ * 1/sqrt(head_dim), attention_sg.wgsl:24; the hybrid passes 1/sqrt(head_dim) as a param).
+ * gate (nullable): [S, H, gate_stride], out = attn / (1 + exp(-gate)) (gate_sigmoid.wgsl:13).
+ * out: [S, H, head_dim] f32. Small S runs the split-K decode kernel, large S the MFMA prefill
+ * kernel; f32 storage runs an exact-f32 kernel. */
+int32_t bg_attention(bg_kv_cache* cache, int32_t layer, const float* q, int32_t S, int32_t H,
+                     int32_t pos_base, float scale, const float* gate, int32_t gate_stride,
+                     float* out, void* stream);
+
+/* Pre-size the split-K workspace for up to S query rows of H heads (otherwise sized on first
+ * use). Call before capturing bg_attention into a HIP graph. */
+int32_t bg_attention_reserve(bg_kv_cache* cache, int32_t S, int32_t H);
+
+/* ---- sink-mode eviction (overflow 'sinks') ------------------------------------------------
+ * evict / evictFor, src/engine.ts:1187-1214. The cache is a ring behind the sinks: eviction
+ * advances the ring head by the reference's batch, so the resident set and its slot order match
+ * the reference's memmove compaction without moving any bytes. */
+int32_t bg_kv_evict(bg_kv_cache* cache, int32_t fill, int32_t need, int32_t* new_fill);
+int32_t bg_kv_evict_for(bg_kv_cache* cache, int32_t fill, int32_t n, int32_t* new_fill);
+
+/* ---- snapshot wire format -----------------------------------------------------------------
+ * Per-region export/import in the reference snapshot layout (src/engine.ts:2724-2734,
+ * 2757-2771, 2847-2860): region BG_K / BG_V is [count, KV, head_dim] elements of the storage
+ * type (f32, f16, or int8 codes = the little-endian bytes of the reference's packed u32 words),
+ * BG_KSCALE / BG_VSCALE is [count, KV, head_dim/32] f32 (q8 only). Positions are logical
+ * slots base .. base+count-1. host: host pointer. Synchronous. */
+int32_t bg_kv_region_bytes(const bg_kv_cache* cache, int32_t region, int32_t count, size_t* bytes);
+int32_t bg_kv_export_rows(bg_kv_cache* cache, int32_t layer, int32_t region, int32_t base,
+                          int32_t count, void* host, void* stream);
+int32_t bg_kv_import_rows(bg_kv_cache* cache, int32_t layer, int32_t region, int32_t base,
+                          int32_t count, const void* host, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BITGPU_ATTN_H */
