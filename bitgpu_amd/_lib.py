@@ -31,6 +31,7 @@ SIGNATURES = [
     ("bg_version", C.c_char_p, []),
     ("bg_rope_tables", _i32, [_f64, _i32, _i32, _f64, _i32, _vp, _vp]),
     ("bg_evict_plan", _i32, [_i32, _i32, _i32, _i32, _pi32, _pi32, _pi32]),
+    ("bg_ring_map", _i32, [_i32, _i32, _i32, _i32, _pi32]),
     ("bg_stream_sync", _i32, [_vp]),
     ("bg_kv_create", _i32, [_i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, C.POINTER(_vp)]),
     ("bg_kv_destroy", _i32, [_vp]),
@@ -44,6 +45,7 @@ SIGNATURES = [
     ("bg_attention_reserve", _i32, [_vp, _i32, _i32]),
     ("bg_kv_evict", _i32, [_vp, _i32, _i32, _pi32]),
     ("bg_kv_evict_for", _i32, [_vp, _i32, _i32, _pi32]),
+    ("bg_kv_ring_state", _i32, [_vp, _pi32, C.POINTER(C.c_int64)]),
     ("bg_kv_region_bytes", _i32, [_vp, _i32, _i32, C.POINTER(C.c_size_t)]),
     ("bg_kv_export_rows", _i32, [_vp, _i32, _i32, _i32, _i32, _vp, _vp]),
     ("bg_kv_import_rows", _i32, [_vp, _i32, _i32, _i32, _i32, _vp, _vp]),

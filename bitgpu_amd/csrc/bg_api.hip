@@ -161,6 +161,20 @@ int32_t bg_evict_plan(int32_t fill, int32_t need, int32_t sinks, int32_t max_seq
   return BG_OK;
 }
 
+int32_t bg_ring_map(int32_t sinks, int32_t max_seq_len, int32_t head, int32_t logical, int32_t* physical) {
+  if (!physical || sinks < 0 || max_seq_len <= sinks || head < 0 || head >= max_seq_len - sinks || logical < 0 ||
+      logical >= max_seq_len)
+    return fail(BG_E_INVALID, "bg_ring_map: bad arguments (sinks %d, max_seq %d, head %d, logical %d)", sinks,
+                max_seq_len, head, logical);
+  bg::Ring r;
+  r.roll = 1;
+  r.sinks = sinks;
+  r.W = max_seq_len - sinks;
+  r.head = head;
+  *physical = r.phys(logical);
+  return BG_OK;
+}
+
 int32_t bg_stream_sync(void* stream) {
   hipError_t e = stream ? hipStreamSynchronize((hipStream_t)stream) : hipDeviceSynchronize();
   return e == hipSuccess ? BG_OK : hip_fail(e, "stream sync");
@@ -417,7 +431,9 @@ int32_t bg_attention(bg_kv_cache* c, int32_t layer, const float* q, int32_t S, i
   if (!(scale > 0.0f) || !std::isfinite(scale)) return fail(BG_E_INVALID, "bg_attention: scale must be positive");
   if (c->roll) {
     if (!c->cos_tab) return fail(BG_E_STATE, "bg_attention: sink mode needs bg_kv_set_rope first");
-    const long need = c->rope_abs ? (long)c->max_seq + c->evicted : (long)c->max_seq;
+    // valid slots are logical < pos_base + S; their rotation index is the slot, or slot +
+    // evicted (absolute mode); masked slots clamp their index inside the table
+    const long need = (long)pos_base + S + (c->rope_abs ? c->evicted : 0);
     if (c->rope_positions < need)
       return fail(BG_E_INVALID, "bg_attention: rope table has %d rows, read-time rotation needs %ld", c->rope_positions, need);
   }
@@ -475,6 +491,13 @@ int32_t bg_kv_evict_for(bg_kv_cache* c, int32_t fill, int32_t n, int32_t* new_fi
   if (!c || !new_fill) return fail(BG_E_INVALID, "bg_kv_evict_for: NULL argument");
   if (c->roll && fill + n > c->max_seq) return bg_kv_evict(c, fill, fill + n - c->max_seq, new_fill);
   *new_fill = fill;
+  return BG_OK;
+}
+
+int32_t bg_kv_ring_state(const bg_kv_cache* c, int32_t* head, int64_t* evicted) {
+  if (!c || !head || !evicted) return fail(BG_E_INVALID, "bg_kv_ring_state: NULL argument");
+  *head = c->head;
+  *evicted = c->evicted;
   return BG_OK;
 }
 

@@ -59,6 +59,27 @@ __device__ inline float code_of(uint32_t w, int byte) { return (float)(int8_t)(w
 
 __device__ inline uint4 ld16(const void* p) { return *(const uint4*)p; }
 
+// Split partials travel between workgroups (possibly on different XCDs, whose L2s are not
+// coherent) as relaxed agent-scope atomics: the stores write through (sc1) and the loads read
+// coherently, so no L2 writeback fence is needed; the writer waits for its stores
+// (vmcnt(0)) before taking the ticket.
+__device__ inline void st_coherent(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ inline float ld_coherent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline void st_coherent2(float* p, float a, float b) {
+  union { float f[2]; uint64_t u; } x;
+  x.f[0] = a;
+  x.f[1] = b;
+  __hip_atomic_store((uint64_t*)p, x.u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline float2 ld_coherent2(const float* p) {
+  union { float f[2]; uint64_t u; } x;
+  x.u = __hip_atomic_load((uint64_t*)const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return make_float2(x.f[0], x.f[1]);
+}
+__device__ inline void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 // which dims lane group g feeds into QK MFMA #t (element e = 0..7 of the lane's half8)
 template <int D, bool QUARTER>
 __device__ inline int qk_dim(int g, int t, int e) {
@@ -87,8 +108,9 @@ struct DecodeParams {
   unsigned* ws_count;  // [KV]
 };
 
-// Shared memory plan (bytes): Q operands, per-wave P^T tiles, per-wave corr, merge buffers.
-template <int D, int DT, bool ROLL, int NSET>
+// Shared memory plan (bytes): Q operands, per-wave P^T tiles, per-wave corr; after the tile
+// loop the same space holds the per-wave partials, then the split merge's weights and sums.
+template <int D, int DT, bool ROLL, int NSET, int NW>
 struct DecodeSmem {
   static constexpr bool QUARTER = (DT == KV_Q8) && !ROLL;
   static constexpr int NT = D / 32;                       // QK MFMAs per 16-slot tile
@@ -106,17 +128,81 @@ struct DecodeSmem {
   }
 };
 
-template <int D, int DT, bool ROLL, int NSET>
-__global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
-  using SM = DecodeSmem<D, DT, ROLL, NSET>;
+// One wave's raw loads for a 32-slot tile (kept in flight while the previous tile computes).
+template <int D, int DT, bool QUARTER>
+struct TileRegs {
+  static constexpr int NB = D / 32;
+  static constexpr int KU = (DT == KV_Q8) ? D / 64 : D / 32;  // uint4 of K per lane per slot
+  static constexpr int VU = (DT == KV_Q8) ? NB : 2 * NB;     // uint4 of V per lane per tile
+  uint4 kr[2][KU];
+  float ksc[2][2];
+  uint4 vr[VU];
+  float vsc[2][DT == KV_Q8 ? NB : 1];
+};
+
+template <int D, int DT, bool QUARTER>
+__device__ __forceinline__ void load_tile(TileRegs<D, DT, QUARTER>& T, int j0, int g, int n,
+                                          const unsigned char* kbase, const unsigned char* vbase,
+                                          const float* ksb, const float* vsb) {
+  constexpr int NB = D / 32;
+  constexpr int KU = TileRegs<D, DT, QUARTER>::KU;
+  constexpr int NSUB = QUARTER ? (D / 128) : 1;
+  constexpr size_t eb = (DT == KV_Q8) ? 1 : 2;
+#pragma unroll
+  for (int t2 = 0; t2 < 2; t2++) {
+    const int P = j0 + 16 * t2 + n;
+    const unsigned char* row = kbase + (size_t)P * D * eb;
+    if constexpr (QUARTER) {
+#pragma unroll
+      for (int i = 0; i < KU; i++) T.kr[t2][i] = ld16(row + g * (D / 4) + 16 * i);
+#pragma unroll
+      for (int i = 0; i < NSUB; i++) T.ksc[t2][i] = ksb[(size_t)P * NB + g * NSUB + i];
+    } else {
+      constexpr int HU = KU / 2;  // uint4 per half piece
+#pragma unroll
+      for (int i = 0; i < HU; i++) {
+        T.kr[t2][i] = ld16(row + (g * (D / 8)) * eb + 16 * i);
+        T.kr[t2][HU + i] = ld16(row + (D / 2 + g * (D / 8)) * eb + 16 * i);
+      }
+      if constexpr (DT == KV_Q8) {
+        T.ksc[t2][0] = ksb[(size_t)P * NB + (g * (D / 8)) / 32];
+        T.ksc[t2][1] = ksb[(size_t)P * NB + (D / 2 + g * (D / 8)) / 32];
+      }
+    }
+    if constexpr (DT == KV_Q8) {
+#pragma unroll
+      for (int b = 0; b < NB; b += 4) {
+        const float4 f = *(const float4*)(vsb + (size_t)P * NB + b);
+        T.vsc[t2][b] = f.x;
+        T.vsc[t2][b + 1] = f.y;
+        T.vsc[t2][b + 2] = f.z;
+        T.vsc[t2][b + 3] = f.w;
+      }
+    }
+  }
+  const unsigned char* vt = vbase + ((size_t)j0 * D + (size_t)g * 8 * D) * eb;
+#pragma unroll
+  for (int b = 0; b < NB; b++) {
+    if constexpr (DT == KV_Q8) {
+      T.vr[b] = ld16(vt + (size_t)(32 * b + 2 * n) * 8);
+    } else {
+      T.vr[2 * b] = ld16(vt + (size_t)(32 * b + 2 * n) * 16);
+      T.vr[2 * b + 1] = ld16(vt + (size_t)(32 * b + 2 * n) * 16 + 16);
+    }
+  }
+}
+
+template <int D, int DT, bool ROLL, int NSET, int NW>
+__global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
+  using SM = DecodeSmem<D, DT, ROLL, NSET, NW>;
   constexpr bool QUARTER = SM::QUARTER;
   constexpr int NT = SM::NT;
   constexpr int NBV = SM::NBV;
   constexpr int RS = SM::RS;
   constexpr int NB = D / 32;         // q8 scale blocks per row
   constexpr int NSUB = QUARTER ? (D / 128) : 1;  // scale blocks inside one lane group's quarter
-  constexpr int KU = (DT == KV_Q8) ? D / 64 : D / 32;  // uint4 of K per lane per slot
-  constexpr int VU = (DT == KV_Q8) ? NB : 2 * NB;     // uint4 of V per lane per tile
+  constexpr int KU = TileRegs<D, DT, QUARTER>::KU;
+  constexpr int NTHR = 64 * NW;
 
   extern __shared__ __align__(16) unsigned char smem[];
   const int tid = threadIdx.x;
@@ -133,8 +219,23 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
   _Float16* pl = (_Float16*)(pbase + wave * (SM::p_bytes_wave + SM::c_bytes_wave));  // [NBV][RS][32]
   float* cl = (float*)((unsigned char*)pl + SM::p_bytes_wave);                         // [RS]
 
+  const Ring ring = p.L.ring;
+  const int cap = p.L.cap;
+  const size_t eb = (DT == KV_Q8) ? 1 : 2;
+  const unsigned char* kbase = (const unsigned char*)p.L.k + (size_t)kvh * cap * D * eb;
+  const unsigned char* vbase = (const unsigned char*)p.L.v + (size_t)kvh * cap * D * eb;
+  const float* ksb = p.L.ks + (size_t)kvh * cap * NB;
+  const float* vsb = p.L.vs + (size_t)kvh * cap * NB;
+
+  const int t_begin = split * p.tiles_per_split;
+  const int t_end = min(t_begin + p.tiles_per_split, p.n_tiles);
+
+  TileRegs<D, DT, QUARTER> A, B;
+  const int tile0 = t_begin + wave;
+  if (tile0 < t_end) load_tile<D, DT, QUARTER>(A, tile0 * 32, g, n, kbase, vbase, ksb, vsb);
+
   // ---- Q operands (block diagonal, hi/lo f16) ----
-  for (int idx = tid; idx < NP * NT * 2 * 64; idx += 256) {
+  for (int idx = tid; idx < NP * NT * 2 * 64; idx += NTHR) {
     const int l = idx & 63, hl = (idx >> 6) & 1, t = (idx >> 7) % NT, pass = (idx >> 7) / NT;
     const int gg = l >> 4, i = l & 15;
     H8 v;
@@ -169,63 +270,8 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
 #pragma unroll
     for (int i = 0; i < D / 16; i++) o[s][i] = floatx4{0, 0, 0, 0};
 
-  const Ring ring = p.L.ring;
-  const int cap = p.L.cap;
-  const size_t eb = (DT == KV_Q8) ? 1 : 2;
-  const unsigned char* kbase = (const unsigned char*)p.L.k + (size_t)kvh * cap * D * eb;
-  const unsigned char* vbase = (const unsigned char*)p.L.v + (size_t)kvh * cap * D * eb;
-  const float* ksb = p.L.ks + (size_t)kvh * cap * NB;
-  const float* vsb = p.L.vs + (size_t)kvh * cap * NB;
-
-  const int t_begin = split * p.tiles_per_split;
-  const int t_end = min(t_begin + p.tiles_per_split, p.n_tiles);
-
-  for (int tile = t_begin + wave; tile < t_end; tile += NW) {
+  auto process = [&](const TileRegs<D, DT, QUARTER>& T, int tile) {
     const int j0 = tile * 32;
-    // ---------------- loads ----------------
-    uint4 kr[2][KU];
-    float ksc[2][2];
-    uint4 vr[VU];
-    float vsc[2][NB];
-#pragma unroll
-    for (int t2 = 0; t2 < 2; t2++) {
-      const int P = j0 + 16 * t2 + n;
-      const unsigned char* row = kbase + (size_t)P * D * eb;
-      if constexpr (QUARTER) {
-#pragma unroll
-        for (int i = 0; i < KU; i++) kr[t2][i] = ld16(row + g * (D / 4) + 16 * i);
-#pragma unroll
-        for (int i = 0; i < NSUB; i++) ksc[t2][i] = ksb[(size_t)P * NB + g * NSUB + i];
-      } else {
-        constexpr int HU = KU / 2;  // uint4 per half piece
-#pragma unroll
-        for (int i = 0; i < HU; i++) {
-          kr[t2][i] = ld16(row + (g * (D / 8)) * eb + 16 * i);
-          kr[t2][HU + i] = ld16(row + (D / 2 + g * (D / 8)) * eb + 16 * i);
-        }
-        if constexpr (DT == KV_Q8) {
-          ksc[t2][0] = ksb[(size_t)P * NB + (g * (D / 8)) / 32];
-          ksc[t2][1] = ksb[(size_t)P * NB + (D / 2 + g * (D / 8)) / 32];
-        }
-      }
-      if constexpr (DT == KV_Q8) {
-#pragma unroll
-        for (int b = 0; b < NB; b++) vsc[t2][b] = vsb[(size_t)P * NB + b];
-      }
-    }
-    {
-      const unsigned char* vt = vbase + ((size_t)j0 * D + (size_t)g * 8 * D) * eb;
-#pragma unroll
-      for (int b = 0; b < NB; b++) {
-        if constexpr (DT == KV_Q8) {
-          vr[b] = ld16(vt + (size_t)(32 * b + 2 * n) * 8);
-        } else {
-          vr[2 * b] = ld16(vt + (size_t)(32 * b + 2 * n) * 16);
-          vr[2 * b + 1] = ld16(vt + (size_t)(32 * b + 2 * n) * 16 + 16);
-        }
-      }
-    }
-
     // ---------------- K operands ----------------
     half8 kb[2][NT];
 #pragma unroll
@@ -234,11 +280,11 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
 #pragma unroll
         for (int t = 0; t < NT; t++) {
           if constexpr (DT == KV_Q8) {
-            const uint4 u = kr[t2][t >> 1];
+            const uint4 u = T.kr[t2][t >> 1];
             kb[t2][t] = (t & 1) ? q8_to_half8(u.z, u.w) : q8_to_half8(u.x, u.y);
           } else {
             H8 h;  // piece 0 holds MFMAs t < NT/2, piece 1 the rest, stored back to back
-            h.u = kr[t2][t];
+            h.u = T.kr[t2][t];
             kb[t2][t] = h.h;
           }
         }
@@ -256,10 +302,10 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
         for (int t = 0; t < HT; t++) {
           float a[8], b2[8];
           if constexpr (DT == KV_Q8) {
-            const uint4 u0 = kr[t2][t >> 1], u1 = kr[t2][KU / 2 + (t >> 1)];
+            const uint4 u0 = T.kr[t2][t >> 1], u1 = T.kr[t2][KU / 2 + (t >> 1)];
             const uint32_t wa0 = (t & 1) ? u0.z : u0.x, wa1 = (t & 1) ? u0.w : u0.y;
             const uint32_t wb0 = (t & 1) ? u1.z : u1.x, wb1 = (t & 1) ? u1.w : u1.y;
-            const float sa = ksc[t2][0] * (1.0f / 127.0f), sb = ksc[t2][1] * (1.0f / 127.0f);
+            const float sa = T.ksc[t2][0] * (1.0f / 127.0f), sb = T.ksc[t2][1] * (1.0f / 127.0f);
 #pragma unroll
             for (int e = 0; e < 4; e++) {
               a[e] = code_of(wa0, e) * sa;
@@ -269,8 +315,8 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
             }
           } else {
             H8 h0, h1;
-            h0.u = kr[t2][t];
-            h1.u = kr[t2][HT + t];
+            h0.u = T.kr[t2][t];
+            h1.u = T.kr[t2][HT + t];
 #pragma unroll
             for (int e = 0; e < 8; e++) { a[e] = (float)h0.h[e]; b2[e] = (float)h1.h[e]; }
           }
@@ -310,9 +356,9 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
 #pragma unroll
         for (int e = 0; e < 4; e++) {
           if constexpr (QUARTER) {
-            float acc = c[0][e] * ksc[t2][0];
+            float acc = c[0][e] * T.ksc[t2][0];
 #pragma unroll
-            for (int i = 1; i < NSUB; i++) acc = fmaf(c[i][e], ksc[t2][i], acc);
+            for (int i = 1; i < NSUB; i++) acc = fmaf(c[i][e], T.ksc[t2][i], acc);
             v[e] = acc;
           } else {
             v[e] = c[0][e];
@@ -356,7 +402,7 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
           const int col = tile_panel(j) * 8 + tile_index(j);
 #pragma unroll
           for (int b = 0; b < NBV; b++) {
-            const float w = (DT == KV_Q8) ? pv * (vsc[t2][b] * (1.0f / 127.0f)) : pv;
+            const float w = (DT == KV_Q8) ? pv * (T.vsc[t2][b] * (1.0f / 127.0f)) : pv;
             pl[((size_t)b * RS + rho) * 32 + col] = (_Float16)w;
           }
         }
@@ -371,12 +417,12 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
 #pragma unroll
     for (int b = 0; b < NB; b++) {
       if constexpr (DT == KV_Q8) {
-        va[b][0] = q8_to_half8(vr[b].x, vr[b].y);
-        va[b][1] = q8_to_half8(vr[b].z, vr[b].w);
+        va[b][0] = q8_to_half8(T.vr[b].x, T.vr[b].y);
+        va[b][1] = q8_to_half8(T.vr[b].z, T.vr[b].w);
       } else {
         H8 e0, e1;
-        e0.u = vr[2 * b];
-        e1.u = vr[2 * b + 1];
+        e0.u = T.vr[2 * b];
+        e1.u = T.vr[2 * b + 1];
         va[b][0] = e0.h;
         va[b][1] = e1.h;
       }
@@ -397,9 +443,22 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+
+  // software pipeline: the next tile's loads are in flight while this one computes. The
+  // prefetch is unconditional (past the end it re-reads the current, cached tile) so the
+  // compiler can count outstanding loads instead of draining them every tile.
+  for (int tile = tile0; tile < t_end; tile += 2 * NW) {
+    const int t1 = tile + NW < t_end ? tile + NW : tile;
+    load_tile<D, DT, QUARTER>(B, t1 * 32, g, n, kbase, vbase, ksb, vsb);
+    process(A, tile);
+    if (tile + NW >= t_end) break;
+    const int t2n = tile + 2 * NW < t_end ? tile + 2 * NW : tile + NW;
+    load_tile<D, DT, QUARTER>(A, t2n * 32, g, n, kbase, vbase, ksb, vsb);
+    process(B, tile + NW);
   }
 
-  // ---------------- combine the 4 waves of the workgroup ----------------
+  // ---------------- combine the waves of the workgroup ----------------
   __syncthreads();
   float* mw = (float*)smem;               // [NW][R]
   float* lw = mw + NW * p.R;              // [NW][R]
@@ -434,7 +493,7 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
   const bool single = p.n_splits == 1;
   float* wso = p.ws_o + ((size_t)kvh * p.n_splits + split) * p.R * D;
   float* wsml = p.ws_ml + ((size_t)kvh * p.n_splits + split) * p.R * 2;
-  for (int idx = tid; idx < p.R * D; idx += 256) {
+  for (int idx = tid; idx < p.R * D; idx += NTHR) {
     const int rho = idx / D, d = idx % D;
     float M = -1e30f;
 #pragma unroll
@@ -452,44 +511,88 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
       if (p.gate) r = r / (1.0f + expf(-p.gate[((size_t)s * p.H + h) * p.gate_stride + d]));
       p.out[((size_t)s * p.H + h) * D + d] = r;
     } else {
-      wso[idx] = acc;
-      if (d == 0) {
-        wsml[2 * rho] = M;
-        wsml[2 * rho + 1] = lt;
-      }
+      st_coherent(&wso[idx], acc);
+      if (d == 0) st_coherent2(&wsml[2 * rho], M, lt);
     }
   }
   if (single) return;
 
   // ---------------- last workgroup of this kv head merges the splits ----------------
   __shared__ unsigned s_last;
-  __threadfence();
+  wait_stores();
   __syncthreads();
   if (tid == 0) {
-    const unsigned prev = atomicAdd(&p.ws_count[kvh], 1u);
+    const unsigned prev = __hip_atomic_fetch_add(&p.ws_count[kvh], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = (prev == (unsigned)(p.n_splits - 1)) ? 1u : 0u;
   }
   __syncthreads();
   if (!s_last) return;
-  __threadfence();
   const float* wo = p.ws_o + (size_t)kvh * p.n_splits * p.R * D;
   const float* wml = p.ws_ml + (size_t)kvh * p.n_splits * p.R * 2;
-  for (int idx = tid; idx < p.R * D; idx += 256) {
-    const int rho = idx / D, d = idx % D;
-    float M = -1e30f;
-    for (int sp = 0; sp < p.n_splits; sp++) M = fmaxf(M, __builtin_nontemporal_load(&wml[((size_t)sp * p.R + rho) * 2]));
-    float acc = 0.0f, lt = 0.0f;
-    for (int sp = 0; sp < p.n_splits; sp++) {
-      const float f = exp2f(__builtin_nontemporal_load(&wml[((size_t)sp * p.R + rho) * 2]) - M);
-      acc += __builtin_nontemporal_load(&wo[((size_t)sp * p.R + rho) * D + d]) * f;
-      lt += __builtin_nontemporal_load(&wml[((size_t)sp * p.R + rho) * 2 + 1]) * f;
-    }
-    const int s = rho / p.G, h = kvh * p.G + rho % p.G;
-    float r = acc / lt;
-    if (p.gate) r = r / (1.0f + expf(-p.gate[((size_t)s * p.H + h) * p.gate_stride + d]));
-    p.out[((size_t)s * p.H + h) * D + d] = r;
+  const int NS = p.n_splits;
+  // (1) per-split weights w[sp][row] = exp2(m_sp - M) / L into LDS
+  float* wts = (float*)smem;                   // [NS][R]
+  float* lsp = wts + NS * p.R;                 // [NS][R]
+  for (int i = tid; i < NS * p.R; i += NTHR) {
+    const float2 ml = ld_coherent2(&wml[2 * i]);
+    wts[i] = ml.x;
+    lsp[i] = ml.y;
   }
-  if (tid == 0) p.ws_count[kvh] = 0u;  // ready for the next launch
+  __syncthreads();
+  for (int rho = tid; rho < p.R; rho += NTHR) {
+    float M = -1e30f;
+    for (int sp = 0; sp < NS; sp++) M = fmaxf(M, wts[sp * p.R + rho]);
+    float L = 0.0f;
+    for (int sp = 0; sp < NS; sp++) L += lsp[sp * p.R + rho] * exp2f(wts[sp * p.R + rho] - M);
+    const float inv = 1.0f / L;
+    for (int sp = 0; sp < NS; sp++) wts[sp * p.R + rho] = exp2f(wts[sp * p.R + rho] - M) * inv;
+  }
+  __syncthreads();
+  // (2) weighted sum of the split partials: float4 columns, TPC threads per column
+  const int C4 = p.R * D / 4;
+  const int TPC = NTHR >= C4 ? NTHR / C4 : 1;
+  const int CPT = NTHR / TPC;                  // columns per pass
+  float4* red = (float4*)(lsp + NS * p.R);     // [TPC][C4] partial sums
+  for (int c0 = 0; c0 < C4; c0 += CPT) {
+    const int c = c0 + tid % CPT;
+    const int k = tid / CPT;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (c < C4 && k < TPC) {
+      const int rho = (4 * c) / D;
+#pragma unroll 8
+      for (int sp = k; sp < NS; sp += TPC) {
+        const float* src = wo + (size_t)sp * p.R * D + 4 * c;
+        const float2 a = ld_coherent2(src), b = ld_coherent2(src + 2);
+        const float w = wts[sp * p.R + rho];
+        acc.x += a.x * w;
+        acc.y += a.y * w;
+        acc.z += b.x * w;
+        acc.w += b.y * w;
+      }
+      red[(size_t)k * C4 + c] = acc;
+    }
+    __syncthreads();
+    if (k == 0 && c < C4) {
+      for (int kk = 1; kk < TPC; kk++) {
+        const float4 v = red[(size_t)kk * C4 + c];
+        acc.x += v.x;
+        acc.y += v.y;
+        acc.z += v.z;
+        acc.w += v.w;
+      }
+      const int rho = (4 * c) / D, d = (4 * c) % D;
+      const int s = rho / p.G, h = kvh * p.G + rho % p.G;
+      float r[4] = {acc.x, acc.y, acc.z, acc.w};
+      if (p.gate) {
+        const float* gr = p.gate + ((size_t)s * p.H + h) * p.gate_stride + d;
+#pragma unroll
+        for (int e = 0; e < 4; e++) r[e] = r[e] / (1.0f + expf(-gr[e]));
+      }
+      *(float4*)(p.out + ((size_t)s * p.H + h) * D + d) = make_float4(r[0], r[1], r[2], r[3]);
+    }
+    __syncthreads();
+  }
+  if (tid == 0) __hip_atomic_store(&p.ws_count[kvh], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // ready for the next launch
 }
 
 // ------------------------------------------------------------------------------------------
@@ -503,37 +606,39 @@ bool decode_supported(const LayerView& L, int S, int H) {
   return R >= 1 && nset_for(R) <= 3;
 }
 
+// waves per workgroup: 8 where the registers allow two workgroups' worth per CU, else 4
+static int waves_for(int D, int nset) { return (D == 128 && nset == 1) ? 8 : 4; }
+
 struct Split { int n_tiles, tps, n_splits, n_scan, phys_limit; };
 
-static Split plan_split(const LayerView& L, int S, int pos_base, int num_cus) {
+static Split plan_split(const LayerView& L, int S, int pos_base, int num_cus, int nw) {
   Split s;
-  if (L.ring.roll && L.ring.head != 0) {
-    s.n_scan = L.max_seq;
-  } else {
-    s.n_scan = pos_base + S;
-  }
+  s.n_scan = (L.ring.roll && L.ring.head != 0) ? L.max_seq : pos_base + S;
   s.phys_limit = L.ring.roll ? L.max_seq : L.cap;
   s.n_tiles = (s.n_scan + 31) / 32;
-  const int target = 2 * (num_cus > 0 ? num_cus : 256);  // workgroups
-  int tps = (s.n_tiles * L.kv_heads + target - 1) / target;
-  tps = tps < NW ? NW : tps;
+  const int cus = num_cus > 0 ? num_cus : 256;
+  // one workgroup per CU: tiles_per_split = ceil(tiles * KV / CUs), at least one tile per wave
+  int tps = (s.n_tiles * L.kv_heads + cus - 1) / cus;
+  tps = tps < nw ? nw : tps;
   s.tps = tps;
   s.n_splits = (s.n_tiles + tps - 1) / tps;
   return s;
 }
 
 size_t decode_workspace_floats(const LayerView& L, int S, int H, int num_cus, size_t* counters) {
-  // upper bound over every pos_base: tiles_per_split >= NW, so at most cap/32/NW splits
+  // upper bound over every pos_base: tiles_per_split >= 4 waves, so at most cap/32/4 splits
   (void)num_cus;
   const int R = (H / L.kv_heads) * S;
-  const int ns_max = (L.cap / 32 + NW - 1) / NW;
+  const int ns_max = (L.cap / 32 + 3) / 4;
   *counters = (size_t)L.kv_heads;
   return (size_t)L.kv_heads * ns_max * R * ((size_t)L.D + 2);
 }
 
 template <int D, int DT, bool ROLL, int NSET>
-static hipError_t launch_cfg(const LayerView& L, const AttnArgs& a, const Split& sp, hipStream_t st) {
-  using SM = DecodeSmem<D, DT, ROLL, NSET>;
+static hipError_t launch_cfg(const LayerView& L, const AttnArgs& a, hipStream_t st) {
+  constexpr int NW = (D == 128 && NSET == 1) ? 8 : 4;
+  using SM = DecodeSmem<D, DT, ROLL, NSET, NW>;
+  const Split sp = plan_split(L, a.S, a.pos_base, a.num_cus, NW);
   DecodeParams p;
   p.L = L;
   p.q = a.q;
@@ -551,43 +656,54 @@ static hipError_t launch_cfg(const LayerView& L, const AttnArgs& a, const Split&
   p.n_tiles = sp.n_tiles;
   p.tiles_per_split = sp.tps;
   p.n_splits = sp.n_splits;
+  const size_t need = (size_t)L.kv_heads * sp.n_splits * p.R * ((size_t)D + 2);
+  if (sp.n_splits > 1 && (a.ws_o == nullptr || need > a.ws_floats)) return hipErrorInvalidValue;
   p.ws_o = a.ws_o;
   p.ws_ml = a.ws_o ? a.ws_o + (size_t)L.kv_heads * sp.n_splits * p.R * D : nullptr;
   p.ws_count = a.ws_count;
   const int NP = (p.R + 3) / 4;
-  const size_t smem = SM::total(NP, p.R);
+  size_t smem = SM::total(NP, p.R);
+  // the split merge reuses the space: weights + l [NS][R] and float4 partial sums
+  const size_t C4 = (size_t)p.R * D / 4;
+  const size_t tpc = (size_t)64 * NW >= C4 ? (size_t)64 * NW / C4 : 1;
+  const size_t merge = (size_t)2 * sp.n_splits * p.R * 4 + tpc * C4 * 16;
+  smem = smem > merge ? smem : merge;
   if (smem > 160 * 1024) return hipErrorInvalidValue;
-  (void)hipFuncSetAttribute((const void*)decode_kernel<D, DT, ROLL, NSET>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
-  hipLaunchKernelGGL((decode_kernel<D, DT, ROLL, NSET>), dim3(sp.n_splits * L.kv_heads), dim3(256), smem, st, p);
+  if (smem > 64 * 1024) {
+    static size_t attr_bytes = 0;
+    if (smem > attr_bytes) {
+      hipError_t e = hipFuncSetAttribute((const void*)decode_kernel<D, DT, ROLL, NSET, NW>,
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+      if (e != hipSuccess) return e;
+      attr_bytes = smem;
+    }
+  }
+  hipLaunchKernelGGL((decode_kernel<D, DT, ROLL, NSET, NW>), dim3(sp.n_splits * L.kv_heads), dim3(64 * NW), smem, st, p);
   return hipGetLastError();
 }
 
 template <int D, int DT, bool ROLL>
-static hipError_t launch_nset(const LayerView& L, const AttnArgs& a, const Split& sp, int nset, hipStream_t st) {
+static hipError_t launch_nset(const LayerView& L, const AttnArgs& a, int nset, hipStream_t st) {
   switch (nset) {
-    case 1: return launch_cfg<D, DT, ROLL, 1>(L, a, sp, st);
-    case 2: return launch_cfg<D, DT, ROLL, 2>(L, a, sp, st);
-    default: return launch_cfg<D, DT, ROLL, 3>(L, a, sp, st);
+    case 1: return launch_cfg<D, DT, ROLL, 1>(L, a, st);
+    case 2: return launch_cfg<D, DT, ROLL, 2>(L, a, st);
+    default: return launch_cfg<D, DT, ROLL, 3>(L, a, st);
   }
 }
 
 template <int D>
-static hipError_t launch_d(const LayerView& L, const AttnArgs& a, const Split& sp, int nset, hipStream_t st) {
+static hipError_t launch_d(const LayerView& L, const AttnArgs& a, int nset, hipStream_t st) {
   const bool roll = L.ring.roll != 0;
   if (L.dtype == KV_Q8) {
-    return roll ? launch_nset<D, KV_Q8, true>(L, a, sp, nset, st) : launch_nset<D, KV_Q8, false>(L, a, sp, nset, st);
+    return roll ? launch_nset<D, KV_Q8, true>(L, a, nset, st) : launch_nset<D, KV_Q8, false>(L, a, nset, st);
   }
-  return roll ? launch_nset<D, KV_F16, true>(L, a, sp, nset, st) : launch_nset<D, KV_F16, false>(L, a, sp, nset, st);
+  return roll ? launch_nset<D, KV_F16, true>(L, a, nset, st) : launch_nset<D, KV_F16, false>(L, a, nset, st);
 }
 
 hipError_t launch_attention_decode(const LayerView& L, const AttnArgs& a, hipStream_t st) {
-  Split sp = plan_split(L, a.S, a.pos_base, a.num_cus);
   const int R = (a.H / L.kv_heads) * a.S;
-  // the split partials must fit the workspace the host sized
-  const size_t need = (size_t)L.kv_heads * sp.n_splits * R * ((size_t)L.D + 2);
-  if (sp.n_splits > 1 && (a.ws_o == nullptr || need > a.ws_floats)) return hipErrorInvalidValue;
   const int nset = nset_for(R);
-  return L.D == 128 ? launch_d<128>(L, a, sp, nset, st) : launch_d<256>(L, a, sp, nset, st);
+  return L.D == 128 ? launch_d<128>(L, a, nset, st) : launch_d<256>(L, a, nset, st);
 }
 
 }  // namespace bg

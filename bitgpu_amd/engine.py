@@ -26,7 +26,7 @@ from ._lib import (BG_K, BG_KSCALE, BG_ROPE_ABSOLUTE, BG_ROPE_SLOT, BG_V, BG_VSC
                    lib)
 
 __all__ = ["KvCache", "attention", "qkv_prologue", "layer_attention", "hybrid_full_attention",
-           "rope_tables", "evict_plan"]
+           "rope_tables", "evict_plan", "ring_map"]
 
 
 def _stream():
@@ -68,6 +68,13 @@ def evict_plan(fill: int, need: int, sinks: int, max_seq_len: int):
     nf, b, k = C.c_int32(), C.c_int32(), C.c_int32()
     check(lib().bg_evict_plan(fill, need, sinks, max_seq_len, C.byref(nf), C.byref(b), C.byref(k)))
     return nf.value, b.value, k.value
+
+
+def ring_map(sinks: int, max_seq_len: int, head: int, logical: int) -> int:
+    """Physical slot of a logical slot in the sink-mode ring (bg_ring_map)."""
+    out = C.c_int32()
+    check(lib().bg_ring_map(sinks, max_seq_len, head, logical, C.byref(out)))
+    return out.value
 
 
 class KvCache:
@@ -149,6 +156,12 @@ class KvCache:
         nf = C.c_int32()
         check(lib().bg_kv_evict_for(self._h, int(fill), int(n), C.byref(nf)))
         return nf.value
+
+    def ring_state(self):
+        """(ring head, rows evicted so far)."""
+        h, e = C.c_int32(), C.c_int64()
+        check(lib().bg_kv_ring_state(self._h, C.byref(h), C.byref(e)))
+        return h.value, e.value
 
     # -- snapshot byte format ----------------------------------------------------------------
     def region_bytes(self, region: int, count: int) -> int:

@@ -65,6 +65,12 @@ int32_t bg_rope_tables(double theta, int32_t rot_dim, int32_t positions, double 
 int32_t bg_evict_plan(int32_t fill, int32_t need, int32_t sinks, int32_t max_seq_len,
                       int32_t* new_fill, int32_t* batch, int32_t* keep);
 
+/* Sink-mode ring map (host-only): the physical slot holding logical slot `logical` when the
+ * ring origin is `head` (logical slots < sinks are fixed; the rest rotate through
+ * max_seq_len - sinks slots). With bg_evict_plan it reproduces the reference's compaction
+ * (src/engine.ts:1206-1209) as pure index arithmetic. */
+int32_t bg_ring_map(int32_t sinks, int32_t max_seq_len, int32_t head, int32_t logical, int32_t* physical);
+
 /* Synchronize a stream (NULL = device). */
 int32_t bg_stream_sync(void* stream);
 
@@ -143,6 +149,10 @@ int32_t bg_attention_reserve(bg_kv_cache* cache, int32_t S, int32_t H);
  * the reference's memmove compaction without moving any bytes. */
 int32_t bg_kv_evict(bg_kv_cache* cache, int32_t fill, int32_t need, int32_t* new_fill);
 int32_t bg_kv_evict_for(bg_kv_cache* cache, int32_t fill, int32_t n, int32_t* new_fill);
+
+/* Ring origin and the number of rows evicted so far (absolute position of logical slot
+ * L >= sinks is L + evicted). */
+int32_t bg_kv_ring_state(const bg_kv_cache* cache, int32_t* head, int64_t* evicted);
 
 /* ---- snapshot wire format -----------------------------------------------------------------
  * Per-region export/import in the reference snapshot layout (src/engine.ts:2724-2734,

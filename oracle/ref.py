@@ -196,8 +196,10 @@ def q8_dequant(codes: np.ndarray, scales: np.ndarray, block: int = Q8_BLOCK) -> 
 
 
 def f16_pack(x: np.ndarray) -> np.ndarray:
-    """f16 cache append, shaders/copy_kv16.wgsl:13 (IEEE round-to-nearest-even)."""
-    return np.asarray(x, f32).astype(np.float16)
+    """f16 cache append, shaders/copy_kv16.wgsl:13 (IEEE round-to-nearest-even; values beyond
+    the f16 range become +-inf)."""
+    with np.errstate(over="ignore"):
+        return np.asarray(x, f32).astype(np.float16)
 
 
 def kv_roundtrip(x: np.ndarray, dtype: str) -> np.ndarray:

@@ -1,0 +1,158 @@
+"""GPU: KV-cache writes are bit-exact with the reference quantizers, and the cache lifecycle
+(growth with rollback, snapshot export/import, sink-mode ring writes) preserves every byte.
+
+Bars: f32 rows bit-identical, f16 rows = IEEE RNE bits (shaders/copy_kv16.wgsl:13), q8 codes
+and scales bit-identical to the WGSL pack4x8snorm quantizer (shaders/copy_kv8.wgsl:24-40)."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from bitgpu_amd import GpuOutOfMemoryError
+from bitgpu_amd import engine as E
+from bitgpu_amd._lib import BG_K, BG_V, BitgpuError
+from oracle import ref
+from tests.gpu_helpers import export_k_v, fill_cache_raw, run_attention, t
+
+pytestmark = pytest.mark.gpu
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _rows(L, KV, D, seed):
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((L, KV, D)) * np.exp(rng.uniform(-6, 6, (L, KV, 1)))).astype(np.float32)
+    x[0] = 0.0                                    # all-zero rows: scale 1e-30, codes 0
+    x[1, 0] = -0.0
+    g = np.load(os.path.join(ROOT, "tests", "golden", "q8_cases.npz"))["x"]   # golden special rows
+    if D == 128:
+        n = min(len(g), L - 2)
+        x[2:2 + n, 0] = g[:n]
+    return x
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16", "q8"])
+@pytest.mark.parametrize("D", [128, 256])
+def test_kv_write_bit_exact(dev, dtype, D):
+    L, KV = 70, 4
+    k, v = _rows(L, KV, D, 1), _rows(L, KV, D, 2)
+    c = E.KvCache(2, KV, D, dtype, max_seq_len=256, capacity=L)
+    # two appends: rows of positions [0, 37) then [37, 70) at dstRow0 = 37 * KV
+    c.append_kv(t(k[:37]), BG_K, 1, 37 * KV, 0)
+    c.append_kv(t(k[37:]), BG_K, 1, (L - 37) * KV, 37 * KV)
+    c.append_kv(t(v), BG_V, 1, L * KV, 0)
+    torch.cuda.synchronize()
+    ek, ev, eks, evs = export_k_v(c, 1, 0, L)
+    if dtype == "f32":
+        assert np.array_equal(ek.view(np.uint32), k.view(np.uint32))
+        assert np.array_equal(ev.view(np.uint32), v.view(np.uint32))
+    elif dtype == "f16":
+        assert np.array_equal(ek.view(np.uint16), ref.f16_pack(k).view(np.uint16))
+        assert np.array_equal(ev.view(np.uint16), ref.f16_pack(v).view(np.uint16))
+    else:
+        ck, sk = ref.q8_pack(k)
+        cv, sv = ref.q8_pack(v)
+        assert np.array_equal(ek, ck) and np.array_equal(eks.view(np.uint32), sk.view(np.uint32))
+        assert np.array_equal(ev, cv) and np.array_equal(evs.view(np.uint32), sv.view(np.uint32))
+    c.close()
+
+
+def test_grow_preserves_content_and_doubles(dev):
+    KV, D = 4, 128
+    c = E.KvCache(2, KV, D, "q8", max_seq_len=1000, capacity=64)
+    k, v = _rows(64, KV, D, 3), _rows(64, KV, D, 4)
+    fill_cache_raw(c, 0, k, v)
+    before = export_k_v(c, 0, 0, 64)
+    c.ensure_capacity(70)                          # doubling: max(70, 128) = 128
+    assert c.capacity == 128
+    after = export_k_v(c, 0, 0, 64)
+    for a, b in zip(before, after):
+        assert np.array_equal(a, b)
+    c.ensure_capacity(5000)                        # clamped to maxSeqLen
+    assert c.capacity == 1000
+    c.close()
+
+
+def test_grow_oom_rolls_back(dev, monkeypatch):
+    KV, D = 4, 128
+    c = E.KvCache(2, KV, D, "f16", max_seq_len=1000, capacity=64)
+    k, v = _rows(64, KV, D, 5), _rows(64, KV, D, 6)
+    fill_cache_raw(c, 1, k, v)
+    monkeypatch.setenv("BG_FAULT_GROW_ALLOC", "3")     # third allocation of the growth fails
+    with pytest.raises(GpuOutOfMemoryError, match="KV cache growth"):
+        c.ensure_capacity(200)
+    monkeypatch.delenv("BG_FAULT_GROW_ALLOC")
+    assert c.capacity == 64
+    ek, ev, _, _ = export_k_v(c, 1, 0, 64)
+    assert np.array_equal(ek.view(np.uint16), ref.f16_pack(k).view(np.uint16))
+    # the cache stays usable
+    q = np.random.default_rng(0).standard_normal((1, 8, D)).astype(np.float32)
+    out = run_attention(c, 1, q, 63)
+    assert np.isfinite(out).all()
+    c.ensure_capacity(200)
+    assert c.capacity == 200
+    c.close()
+
+
+@pytest.mark.parametrize("dtype", ["f32", "q8"])
+def test_snapshot_roundtrip_into_fresh_cache(dev, dtype):
+    KV, D, L = 8, 128, 300
+    a = E.KvCache(3, KV, D, dtype, max_seq_len=512, capacity=512)
+    for li in range(3):
+        fill_cache_raw(a, li, _rows(L, KV, D, 10 + li), _rows(L, KV, D, 20 + li))
+    snap = a.save_snapshot(L)
+    per_row = KV * D * (4 if dtype == "f32" else 1) + (KV * D // 32 * 4 if dtype == "q8" else 0)
+    assert len(snap) == 3 * 2 * L * per_row            # src/engine.ts:2732-2733 snapshotBytes
+    b = E.KvCache(3, KV, D, dtype, max_seq_len=512)    # fresh, smaller initial capacity
+    b.restore_snapshot(snap, L)
+    q = np.random.default_rng(1).standard_normal((1, 32, D)).astype(np.float32)
+    for li in range(3):
+        for x, y in zip(export_k_v(a, li, 0, L), export_k_v(b, li, 0, L)):
+            if x is not None:
+                assert np.array_equal(x, y)
+        assert np.array_equal(run_attention(a, li, q, L - 1), run_attention(b, li, q, L - 1))
+    # delta snapshot: positions [base, L)
+    d = a.save_snapshot(L, base=100)
+    cpart = E.KvCache(3, KV, D, dtype, max_seq_len=512, capacity=512)
+    for li in range(3):
+        fill_cache_raw(cpart, li, _rows(L, KV, D, 10 + li)[:100], _rows(L, KV, D, 20 + li)[:100])
+    cpart.restore_snapshot(d, L, base=100)
+    for li in range(3):
+        assert np.array_equal(run_attention(a, li, q, L - 1), run_attention(cpart, li, q, L - 1))
+    with pytest.raises(ValueError, match="expected"):
+        b.restore_snapshot(snap[:-4], L)
+    for x in (a, b, cpart):
+        x.close()
+
+
+def test_sink_ring_writes_land_at_logical_slots(dev):
+    KV, D, sinks, max_seq = 2, 128, 4, 100
+    c = E.KvCache(1, KV, D, "q8", max_seq_len=max_seq, overflow="sinks", sink_tokens=sinks)
+    rows = _rows(max_seq, KV, D, 7)
+    fill_cache_raw(c, 0, rows, rows)
+    fill = c.evict_for(max_seq, 10)                    # evicts a quarter-window batch
+    nf, batch, keep = ref.evict(max_seq, 10, sinks, max_seq)
+    assert fill == nf and c.ring_state() == (batch, batch)
+    kept = np.concatenate([rows[:sinks], rows[sinks + batch: sinks + batch + keep]])
+    ck, sk = ref.q8_pack(kept)
+    ek, _, eks, _ = export_k_v(c, 0, 0, fill)
+    assert np.array_equal(ek, ck) and np.array_equal(eks, sk)
+    new = _rows(max_seq - fill, KV, D, 8)               # these wrap around the physical ring
+    fill_cache_raw(c, 0, new, new, row0=fill)
+    ek, _, _, _ = export_k_v(c, 0, fill, max_seq - fill)
+    assert np.array_equal(ek, ref.q8_pack(new)[0])
+    c.close()
+
+
+def test_argument_errors_are_raised_not_faulted(dev):
+    c = E.KvCache(1, 8, 128, "f16", max_seq_len=256, capacity=64)
+    q = t(np.zeros((1, 32, 128), np.float32))
+    with pytest.raises(BitgpuError, match="exceed the cache"):
+        E.attention(c, 0, q, 1, 32, 64)                # position 64 is beyond capacity 64
+    with pytest.raises(BitgpuError, match="out of range"):
+        E.attention(c, 3, q, 1, 32, 0)
+    with pytest.raises(BitgpuError, match="multiple of kv_heads|heads"):
+        E.attention(c, 0, t(np.zeros((1, 12, 128), np.float32)), 1, 12, 0)
+    with pytest.raises(BitgpuError, match="beyond capacity"):
+        c.append_kv(t(np.zeros((8, 128), np.float32)), BG_K, 0, 8, 64 * 8)
+    c.close()
