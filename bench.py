@@ -1,0 +1,375 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X attention hot path (BASELINE.json metric).
+
+Headline (`value`): decode attention over a q8 KV cache at 32k context in the Qwen3-8B/4B
+attention shape (32 query heads, 8 KV heads, head_dim 128), swept over 36 distinct layers
+(config C3), as HBM GB/s of algorithmic bytes; `us_per_layer` is the same measurement as time.
+One "step" = one decode token's attention over all 36 layers (36 kernel launches, replayed as a
+HIP graph; the cache is resident in HBM before the timed region). Also reported: the 4k/16k
+sweeps, C2 causal prefill TFLOP/s, C1 f32 decode, C4 sink-mode decode/verify, C5 hybrid
+prefill + decode, and the oracle numpy path timed on this host's cores.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--quick]
+
+Only one GPU is used: --gpus above 1 exits with a message.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+MFMA_F16_PEAK_TFLOPS = 2516.6  # MI355X dense fp16/bf16 MFMA
+
+
+def c3_bytes(L, KV=8, D=128, H=32):
+    """Algorithmic bytes of one decode-attention layer over a q8 cache: K and V codes plus one
+    f32 scale per 32 values, and the f32 query and output."""
+    return L * KV * 2 * (D + 4 * D // 32) + 2 * H * D * 4
+
+
+def causal_flops(S, H, D, past=0):
+    """QK^T and PV FLOPs of a causal prefill: 2 * 2 * D * H * sum_s (past + s + 1)."""
+    return 2 * 2 * D * H * (S * past + S * (S + 1) // 2)
+
+
+def graph_replay_us(torch, fn, steps, warmup):
+    """Capture fn() into a HIP graph; replay warmup times untimed, then time `steps` replays
+    bracketed by synchronize. Returns microseconds per replay."""
+    fn()
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        fn()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            fn()
+    torch.cuda.synchronize()
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / steps
+
+
+class DecodeSweep:
+    """36 distinct q8 layer caches at context L, filled through the fused prologue."""
+
+    def __init__(self, torch, E, W, L, layers=36, seed=3):
+        cfg = W.C3
+        self.L, self.layers, self.cfg = L, layers, cfg
+        q, k, v = W.draw(seed, (1, cfg.H, cfg.D), (L, cfg.KV, cfg.D), (L, cfg.KV, cfg.D))
+        self.q_host, self.k_host, self.v_host = q, k, v
+        dev = "cuda"
+        self.cos, self.sin = (torch.from_numpy(x).to(dev) for x in E.rope_tables(cfg.theta, cfg.rot, L))
+        self.ones = torch.ones(cfg.D, device=dev)
+        self.cache = E.KvCache(layers, cfg.KV, cfg.D, cfg.kv, max_seq_len=L, capacity=L)
+        kt = torch.from_numpy(k).to(dev)
+        vt = torch.from_numpy(v).to(dev)
+        qt = torch.from_numpy(q).to(dev)
+        for li in range(layers):
+            E.qkv_prologue(self.cache, li, None, kt[: L - 1], vt[: L - 1], L - 1, cfg.H, None, self.ones, cfg.eps,
+                           self.cos, self.sin, cfg.rot, 0, 0)
+        self.qt, self.kt, self.vt = qt, kt[L - 1:].contiguous(), vt[L - 1:].contiguous()
+        self.qr = torch.empty(1, cfg.H, cfg.D, device=dev)
+        self.out = torch.empty(1, cfg.H, cfg.D, device=dev)
+        self.E = E
+        for li in range(layers):
+            self.prologue(li)
+        self.cache_attn_reserve()
+
+    def cache_attn_reserve(self):
+        from bitgpu_amd._lib import check, lib
+        check(lib().bg_attention_reserve(self.cache.handle, 1, self.cfg.H))
+
+    def prologue(self, li):
+        cfg = self.cfg
+        self.E.qkv_prologue(self.cache, li, self.qt, self.kt, self.vt, 1, cfg.H, self.ones, self.ones, cfg.eps,
+                            self.cos, self.sin, cfg.rot, self.L - 1, self.L - 1, q_out=self.qr)
+
+    def attention(self, li):
+        self.E.attention(self.cache, li, self.qr, 1, self.cfg.H, self.L - 1, out=self.out)
+
+    def sweep(self):
+        for li in range(self.layers):
+            self.attention(li)
+
+    def full_step(self):
+        for li in range(self.layers):
+            self.prologue(li)
+            self.attention(li)
+
+    def close(self):
+        self.cache.close()
+
+
+def cpu_baseline(sweep, W, budget_s=12.0):
+    """The oracle numpy path (tools/reference.py:158-175 restated, q8 dequant first) on this
+    host's cores, one layer of the headline workload per repetition; best of the repetitions
+    that fit the time budget."""
+    from oracle import ref
+    cfg = W.C3
+    L = sweep.L
+    cos, sin = ref.rope_tables(cfg.theta, cfg.rot, L)
+    ones = np.ones(cfg.D, np.float32)
+    kr = ref.norm_rope(sweep.k_host, ones, cfg.eps, cos, sin, np.arange(L))
+    kc, ks = ref.q8_pack(kr)
+    vc, vs = ref.q8_pack(sweep.v_host)
+    qr = ref.norm_rope(sweep.q_host, ones, cfg.eps, cos, sin, [L - 1])
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 2:
+        t0 = time.perf_counter()
+        kk = ref.q8_dequant(kc, ks)
+        vv = ref.q8_dequant(vc, vs)
+        ref.attention(qr, kk, vv, L - 1)
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 5:
+            break
+    best = min(times)
+    cores = os.cpu_count()
+    return {
+        "value": round(c3_bytes(L) / best / 1e9, 3),
+        "unit": "GB/s",
+        "us_per_layer": round(best * 1e6, 1),
+        "cores": cores,
+        "kind": "port",
+        "sample": f"one layer of the C3 32k q8 decode (numpy oracle: q8 dequant + GQA softmax attention in "
+                  f"float64), best of {len(times)}; numpy BLAS threads = all {cores} host cores",
+    }
+
+
+def bench_prefill(torch, E, W, cfg, S, steps, warmup, seed):
+    q, k, v, g = W.prefill_inputs(cfg, S, seed)
+    dev = "cuda"
+    c = E.KvCache(1, cfg.KV, cfg.D, cfg.kv, max_seq_len=S, capacity=S)
+    cos, sin = (torch.from_numpy(x).to(dev) for x in E.rope_tables(cfg.theta, cfg.rot, S))
+    ones = torch.ones(cfg.D, device=dev)
+    qt, kt, vt = (torch.from_numpy(x).to(dev) for x in (q, k, v))
+    gt = torch.from_numpy(g).to(dev) if g is not None else None
+    qr = torch.empty(S, cfg.H, cfg.D, device=dev)
+    out = torch.empty(S, cfg.H, cfg.D, device=dev)
+    scale = float(1.0 / np.sqrt(cfg.D))
+
+    def prologue():
+        E.qkv_prologue(c, 0, qt, kt, vt, S, cfg.H, ones, ones, cfg.eps, cos, sin, cfg.rot, 0, 0, q_out=qr)
+
+    def attn():
+        E.attention(c, 0, qr, S, cfg.H, 0, scale=scale, gate=gt, gate_stride=cfg.D if gt is not None else None,
+                    out=out)
+
+    prologue()
+    us_attn = graph_replay_us(torch, attn, steps, warmup)
+    us_pro = graph_replay_us(torch, prologue, steps, warmup)
+    fl = causal_flops(S, cfg.H, cfg.D)
+    c.close()
+    return {"S": S, "attn_us": round(us_attn, 1), "prologue_us": round(us_pro, 1),
+            "tflops": round(fl / us_attn / 1e6, 1), "mfma_frac": round(fl / us_attn / 1e6 / MFMA_F16_PEAK_TFLOPS, 4)}
+
+
+def bench_c1(torch, E, W, steps, warmup):
+    cfg = W.C1
+    q, k, v, _ = W.decode_inputs(cfg, W.C1_PAST, seed=1)
+    dev = "cuda"
+    L = W.C1_PAST + 1
+    c = E.KvCache(28, cfg.KV, cfg.D, cfg.kv, max_seq_len=2048)
+    c.ensure_capacity(L)
+    cos, sin = (torch.from_numpy(x).to(dev) for x in E.rope_tables(cfg.theta, cfg.rot, 2048))
+    ones = torch.ones(cfg.D, device=dev)
+    kt, vt, qt = (torch.from_numpy(x).to(dev) for x in (k, v, q))
+    for li in range(28):
+        E.qkv_prologue(c, li, None, kt[:L], vt[:L], L, cfg.H, None, ones, cfg.eps, cos, sin, cfg.rot, 0, 0)
+    qr = E.qkv_prologue(c, 0, qt, None, None, 1, cfg.H, ones, None, cfg.eps, cos, sin, cfg.rot, W.C1_PAST, W.C1_PAST)
+    out = torch.empty(1, cfg.H, cfg.D, device=dev)
+    us = graph_replay_us(torch, lambda: [E.attention(c, li, qr, 1, cfg.H, W.C1_PAST, out=out) for li in range(28)],
+                         steps, warmup) / 28
+    c.close()
+    B = L * cfg.KV * 2 * cfg.D * 4 + 2 * cfg.H * cfg.D * 4
+    return {"us_per_layer": round(us, 2), "GBs": round(B / us / 1e3, 1), "layers": 28}
+
+
+def bench_c4(torch, E, W, steps, warmup):
+    """Sink mode at position 100000: the ring state after the reference's greedy eviction
+    schedule (index arithmetic only), f16 cache, 4 sinks + 4096 window."""
+    cfg = W.C4
+    sinks, max_seq = cfg.sinks, cfg.sinks + cfg.window
+    dev = "cuda"
+    res = {}
+    for verify in (1, W.C4_VERIFY):
+        c = E.KvCache(1, cfg.KV, cfg.D, cfg.kv, max_seq_len=max_seq, overflow="sinks", sink_tokens=sinks)
+        fill, fed = 1000, 1000
+        while fed < W.C4_POSITION:
+            batch = min(4, W.C4_POSITION - fed)
+            fill = c.evict_for(fill, batch) + batch
+            fed += batch
+        fill = c.evict_for(fill, verify)
+        cos, sin = (torch.from_numpy(x).to(dev) for x in E.rope_tables(cfg.theta, cfg.rot, max_seq))
+        c.set_rope(cos, sin)
+        rng = np.random.default_rng(4)
+        k = torch.from_numpy(rng.standard_normal((fill + verify, cfg.KV, cfg.D)).astype(np.float32)).to(dev)
+        v = torch.from_numpy(rng.standard_normal((fill + verify, cfg.KV, cfg.D)).astype(np.float32)).to(dev)
+        q = torch.from_numpy(rng.standard_normal((verify, cfg.H, cfg.D)).astype(np.float32)).to(dev)
+        ones = torch.ones(cfg.D, device=dev)
+        E.qkv_prologue(c, 0, None, k, v, fill + verify, cfg.H, None, ones, cfg.eps, cos, sin, cfg.rot, 0, 0)
+        qr = E.qkv_prologue(c, 0, q, None, None, verify, cfg.H, ones, None, cfg.eps, cos, sin, cfg.rot, fill, fill)
+        out = torch.empty(verify, cfg.H, cfg.D, device=dev)
+        us = graph_replay_us(torch, lambda: E.attention(c, 0, qr, verify, cfg.H, fill, out=out), steps, warmup)
+        B = (fill + verify) * cfg.KV * 2 * cfg.D * 2 + 2 * verify * cfg.H * cfg.D * 4
+        res["decode" if verify == 1 else f"verify{verify}"] = {"us": round(us, 2), "GBs": round(B / us / 1e3, 1),
+                                                               "resident_slots": fill + verify}
+        c.close()
+    return res
+
+
+def bench_c5_decode(torch, E, W, steps, warmup):
+    cfg = W.C5
+    L = W.C5_PREFILL + 1
+    dev = "cuda"
+    c = E.KvCache(16, cfg.KV, cfg.D, cfg.kv, max_seq_len=W.C5_PREFILL + W.C5_DECODE_STEPS,
+                  capacity=W.C5_PREFILL + W.C5_DECODE_STEPS)
+    rng = np.random.default_rng(5)
+    k = torch.from_numpy(rng.standard_normal((L, cfg.KV, cfg.D)).astype(np.float32)).to(dev)
+    from bitgpu_amd._lib import BG_K, BG_V
+    for li in range(16):
+        c.append_kv(k, BG_K, li, L * cfg.KV, 0)
+        c.append_kv(k, BG_V, li, L * cfg.KV, 0)
+    q = torch.from_numpy(rng.standard_normal((1, cfg.H, cfg.D)).astype(np.float32)).to(dev)
+    g = torch.from_numpy(rng.standard_normal((1, cfg.H, cfg.D)).astype(np.float32)).to(dev)
+    out = torch.empty(1, cfg.H, cfg.D, device=dev)
+    scale = float(1.0 / np.sqrt(cfg.D))
+    us = graph_replay_us(torch, lambda: [E.attention(c, li, q, 1, cfg.H, L - 1, scale=scale, gate=g, gate_stride=cfg.D,
+                                                     out=out) for li in range(16)], steps, warmup) / 16
+    c.close()
+    B = L * cfg.KV * 2 * (cfg.D + 4 * cfg.D // 32) + 3 * cfg.H * cfg.D * 4
+    return {"context": L, "us_per_layer": round(us, 2), "GBs": round(B / us / 1e3, 1)}
+
+
+def load_traffic(name):
+    p = os.path.join(ROOT, "profiles", name)
+    if not os.path.exists(p):
+        return None
+    try:
+        with open(p) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--quick", action="store_true", help="headline only (no extras, no CPU baseline)")
+    ap.add_argument("--profile-loop", type=int, default=0,
+                    help="run only the headline sweep this many times (for rocprofv3 --pmc), print nothing else")
+    ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="run only a device-to-device copy of MIB MiB (3 times) to calibrate the "
+                         "FETCH_SIZE / WRITE_SIZE counters against known bytes")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus > 1 or world > 1:
+        print(f"bench.py: this build measures one GPU only (asked for {max(args.gpus, world)}); "
+              "multi-GPU sharding is a design note, not a benchmark here", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from bitgpu_amd import engine as E
+    from bitgpu_amd import workloads as W
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+
+    if args.calibrate_copy:
+        n = args.calibrate_copy * (1 << 20) // 4
+        a = torch.randn(n, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        return
+
+    L = 32768
+    sweep = DecodeSweep(torch, E, W, L)
+    if args.profile_loop:
+        for _ in range(args.profile_loop):
+            sweep.sweep()
+        torch.cuda.synchronize()
+        sweep.close()
+        return
+
+    us_sweep = graph_replay_us(torch, sweep.sweep, args.steps, args.warmup)
+    us_layer = us_sweep / sweep.layers
+    B = c3_bytes(L)
+    gbs = B / us_layer / 1e3
+    us_full = graph_replay_us(torch, sweep.full_step, max(3, args.steps // 2), args.warmup)
+
+    extra = {}
+    cpu = None
+    if not args.quick:
+        extra["c3_contexts"] = {}
+        for Lx in (4096, 16384):
+            sw = DecodeSweep(torch, E, W, Lx)
+            u = graph_replay_us(torch, sw.sweep, args.steps, args.warmup) / sw.layers
+            extra["c3_contexts"][str(Lx)] = {"us_per_layer": round(u, 2), "GBs": round(c3_bytes(Lx) / u / 1e3, 1),
+                                             "hbm_frac": round(c3_bytes(Lx) / u / 1e3 / HBM_PEAK_GBS, 4)}
+            sw.close()
+        extra["c3_contexts"]["32768"] = {"us_per_layer": round(us_layer, 2), "GBs": round(gbs, 1),
+                                         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+        extra["c2_prefill_f16"] = bench_prefill(torch, E, W, W.C2, W.C2_S, max(3, args.steps // 2), args.warmup, 2)
+        extra["c5_prefill_q8"] = bench_prefill(torch, E, W, W.C5, W.C5_PREFILL, 3, 1, 5)
+        extra["c5_decode_q8"] = bench_c5_decode(torch, E, W, args.steps, args.warmup)
+        extra["c1_decode_f32"] = bench_c1(torch, E, W, args.steps, args.warmup)
+        extra["c4_sinks_f16"] = bench_c4(torch, E, W, args.steps, args.warmup)
+        cpu = cpu_baseline(sweep, W, args.cpu_budget)
+    sweep.close()
+
+    traffic = load_traffic("decode_q8_32k_traffic.json")
+    line = {
+        "metric": "decode-attn HBM GB/s (Qwen3-8B attention shape, 32k ctx, q8 KV, 36 layers)",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(us_sweep / 1e3, 4),
+        "us_per_layer": round(us_layer, 2),
+        "tokens_per_s": round(1e6 / us_sweep, 1),
+        "step_with_prologue_ms": round(us_full / 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q8 KV (int8 codes + f32 scales), f16 MFMA operands, f32 accumulate",
+        "data": "synthetic (seeded N(0,1) K/V, RMSNorm+RoPE through the fused prologue)",
+        "config": {"workload": "C3 decode attention, 36 distinct layers x 32768 cached positions, batch 1",
+                   "heads": 32, "kv_heads": 8, "head_dim": 128, "kv_cache": "q8", "context": L, "layers": 36},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": traffic.get("bytes_per_launch") if traffic else None,
+                     "bytes_per_launch_algorithmic": B},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()
