@@ -15,6 +15,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "lib", "libbitgpu_attn.so")
+NODE_SRC = os.path.join(HERE, "node", "bitgpu_attn_napi.c")
+NODE_OUT = os.path.join(HERE, "node", "bitgpu_attn.node")
+NODE_INC = "/usr/include/node"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 FLAGS = [
@@ -48,7 +51,26 @@ def build(verbose: bool = True) -> str:
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB}")
+    build_node_addon(verbose)
     return LIB
+
+
+def build_node_addon(verbose: bool = True) -> str | None:
+    """The N-API addon for a JS/TypeScript host (needs the Node headers; skipped without them)."""
+    if not os.path.isdir(NODE_INC):
+        if verbose:
+            print("node headers not found; N-API addon not built")
+        return None
+    cmd = ["gcc", "-O2", "-fPIC", "-shared", "-std=c11", "-Wall", f"-I{NODE_INC}", "-DNODE_GYP_MODULE_NAME=bitgpu_attn",
+           NODE_SRC, "-o", NODE_OUT + ".tmp", f"-L{os.path.dirname(LIB)}", "-lbitgpu_attn",
+           "-L/opt/rocm/lib", "-lamdhip64", "-Wl,-rpath,$ORIGIN/../lib", "-Wl,-rpath,/opt/rocm/lib"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"N-API addon build failed:\n{r.stdout}\n{r.stderr}")
+    os.replace(NODE_OUT + ".tmp", NODE_OUT)
+    if verbose:
+        print(f"built {NODE_OUT}")
+    return NODE_OUT
 
 
 if __name__ == "__main__":

@@ -1,0 +1,28 @@
+// Types of the JS shim (index.js) for a TypeScript host. Device pointers and streams are bigint.
+export type DevPtr = bigint
+export declare const K: 0, V: 1, KSCALE: 2, VSCALE: 3
+export declare class GpuOutOfMemoryError extends Error { code?: number }
+export declare function synthRope(theta: number, rotDim: number, positions: number,
+  yarn?: { factor: number; original_max_position_embeddings: number }): [Float32Array, Float32Array]
+export interface KvCacheOptions {
+  layers: number; kvHeads: number; headDim: number
+  kvCache?: 'f32' | 'f16' | 'q8'; maxSeqLen?: number; capacity?: number
+  overflow?: 'error' | 'sinks'; sinkTokens?: number; ropePositions?: 'slot' | 'absolute'
+}
+export declare class KvCache {
+  constructor(opts: KvCacheOptions)
+  readonly capacity: number
+  dispose(): void
+  ensureKvCapacity(needed: number, stream?: DevPtr | null): void
+  setRollTables(cosDev: DevPtr, sinDev: DevPtr, positions: number): void
+  appendKV(srcDev: DevPtr, which: 0 | 1, li: number, rows: number, dstRow0: number, stream?: DevPtr | null): void
+  prologue(a: { li: number; q?: DevPtr | null; qStride?: number; k?: DevPtr | null; v?: DevPtr | null; S: number; H: number
+    qGamma?: DevPtr | null; kGamma?: DevPtr | null; eps: number; cos: DevPtr; sin: DevPtr; ropePositions: number
+    rotDim: number; pos0: number; slot0: number; qOut?: DevPtr | null; stream?: DevPtr | null }): void
+  att(qr: DevPtr, li: number, S: number, H: number, posBase: number, out: DevPtr,
+    o?: { scale?: number; gate?: DevPtr | null; gateStride?: number; stream?: DevPtr | null }): void
+  evict(fill: number, need: number): number
+  evictFor(fill: number, n: number): number
+  exportRows(li: number, region: 0 | 1 | 2 | 3, base: number, count: number): ArrayBuffer
+  importRows(li: number, region: 0 | 1 | 2 | 3, base: number, count: number, buf: ArrayBuffer): void
+}

@@ -1,0 +1,83 @@
+"""The N-API addon + JS shim (bitgpu_amd/node) that a TypeScript engine host would bind:
+host-only entry points on the CPU, and one decode + prefill through the addon on the GPU,
+checked against the oracle."""
+import json
+import os
+import shutil
+import subprocess
+
+import numpy as np
+import pytest
+
+from bitgpu_amd import engine as E
+from oracle import ref
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+NODE_DIR = os.path.join(ROOT, "bitgpu_amd", "node")
+NODE = shutil.which("node")
+
+
+def run_node(script, tmp_path, timeout=120):
+    p = tmp_path / "t.js"
+    p.write_text(f"const b = require({json.dumps(os.path.join(NODE_DIR, 'index.js'))});\n" + script)
+    r = subprocess.run([NODE, str(p)], capture_output=True, text=True, timeout=timeout)
+    assert r.returncode == 0, r.stderr
+    return r.stdout
+
+
+pytestmark_node = pytest.mark.skipif(NODE is None or not os.path.exists(os.path.join(NODE_DIR, "bitgpu_attn.node")),
+                                     reason="node or the built addon is not available")
+
+
+@pytestmark_node
+def test_addon_host_functions(tmp_path):
+    out = run_node("""
+const res = {}
+res.plans = [[4100, 4], [4100, 1], [3000, 9], [200, 500]].map(([f, n]) => b.addon.evictPlan(f, n, 4, 4100))
+res.ring = [0, 3, 4, 100, 4099].map(L => b.addon.ringMap(4, 4100, 1234, L))
+const [c, s] = b.synthRope(1e7, 64, 300)
+res.cos = Array.from(c); res.sin = Array.from(s)
+try { new b.KvCache({layers: 1, kvHeads: 8, headDim: 128, maxSeqLen: 60, overflow: 'sinks'}) } catch (e) { res.err = [e.code, e.message] }
+console.log(JSON.stringify(res))
+""", tmp_path)
+    res = json.loads(out)
+    for (f, n), got in zip([[4100, 4], [4100, 1], [3000, 9], [200, 500]], res["plans"]):
+        assert tuple(got) == ref.evict(f, n, 4, 4100)
+    assert res["ring"] == [E.ring_map(4, 4100, 1234, L) for L in [0, 3, 4, 100, 4099]]
+    c, s = E.rope_tables(1e7, 64, 300)
+    assert np.array_equal(np.array(res["cos"], np.float32), c.ravel())
+    assert np.array_equal(np.array(res["sin"], np.float32), s.ravel())
+    assert res["err"][0] == -1 and "maxSeqLen >= sinkTokens + 64" in res["err"][1]
+
+
+@pytest.mark.gpu
+@pytestmark_node
+@pytest.mark.parametrize("dtype,S", [("q8", 1), ("f16", 70)])
+def test_addon_attention_on_gpu(tmp_path, dtype, S):
+    rng = np.random.default_rng(S)
+    L, H, KV, D = 300, 32, 8, 128
+    k = rng.standard_normal((L, KV, D)).astype(np.float32)
+    v = rng.standard_normal((L, KV, D)).astype(np.float32)
+    q = rng.standard_normal((S, H, D)).astype(np.float32)
+    for name, arr in (("k", k), ("v", v), ("q", q)):
+        arr.tofile(tmp_path / f"{name}.bin")
+    run_node(f"""
+const fs = require('fs')
+const rd = n => {{ const b = fs.readFileSync({json.dumps(str(tmp_path))} + '/' + n + '.bin'); return new Float32Array(b.buffer, b.byteOffset, b.length / 4) }}
+const a = b.addon
+const k = rd('k'), v = rd('v'), q = rd('q')
+const dk = a.devAlloc(k.byteLength), dv = a.devAlloc(v.byteLength), dq = a.devAlloc(q.byteLength), dout = a.devAlloc(q.byteLength)
+a.h2d(dk, k); a.h2d(dv, v); a.h2d(dq, q)
+const c = new b.KvCache({{layers: 2, kvHeads: {KV}, headDim: {D}, kvCache: '{dtype}', maxSeqLen: 512, capacity: {L}}})
+c.appendKV(dk, b.K, 1, {L * KV}, 0)
+c.appendKV(dv, b.V, 1, {L * KV}, 0)
+c.att(dq, 1, {S}, {H}, {L - S}, dout)
+a.sync()
+const out = new Float32Array(q.length)
+a.d2h(out, dout)
+fs.writeFileSync({json.dumps(str(tmp_path))} + '/out.bin', Buffer.from(out.buffer))
+c.dispose()
+""", tmp_path)
+    out = np.fromfile(tmp_path / "out.bin", np.float32).reshape(S, H, D)
+    exp = ref.attention(q, ref.kv_roundtrip(k, dtype), ref.kv_roundtrip(v, dtype), L - S)
+    assert np.abs(out - exp).max() / np.abs(exp).max() <= 2e-3
