@@ -117,7 +117,8 @@ struct DecodeSmem {
   static constexpr int NBV = (DT == KV_Q8) ? D / 32 : 1;  // P copies (one per V scale block)
   static constexpr int RS = 16 * NSET;                    // padded rows
   static constexpr int NPMAX = RS / 4;                    // QK passes
-  __host__ __device__ static size_t q_bytes(int np) { return (size_t)np * NT * 2 * 64 * 16; }
+  // + one 32-byte sink for the stores of operand slots past the last pass
+  __host__ __device__ static size_t q_bytes(int np) { return (size_t)np * NT * 2 * 64 * 16 + 32; }
   static constexpr size_t p_bytes_wave = (size_t)NBV * RS * 32 * 2;
   static constexpr size_t c_bytes_wave = (size_t)RS * 4;
   __host__ __device__ static size_t merge_bytes(int R) { return (size_t)NW * R * (D + 2) * 4; }
@@ -230,28 +231,50 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
   const int t_begin = split * p.tiles_per_split;
   const int t_end = min(t_begin + p.tiles_per_split, p.n_tiles);
 
+  // Q operands (block diagonal, hi/lo f16). The setup is straight-line code -- every load is
+  // unconditional (spare slots read query 0, a wave without tiles re-reads the split's last
+  // tile) and spare slots store to a sink -- so the q gather, issued first, can be waited for
+  // on its own while the first tile's loads stay in flight.
   TileRegs<D, DT, QUARTER> A, B;
   const int tile0 = t_begin + wave;
-  if (tile0 < t_end) load_tile<D, DT, QUARTER>(A, tile0 * 32, g, n, kbase, vbase, ksb, vsb);
-
-  // ---- Q operands (block diagonal, hi/lo f16) ----
-  for (int idx = tid; idx < NP * NT * 2 * 64; idx += NTHR) {
-    const int l = idx & 63, hl = (idx >> 6) & 1, t = (idx >> 7) % NT, pass = (idx >> 7) / NT;
-    const int gg = l >> 4, i = l & 15;
-    H8 v;
-    v.u = make_uint4(0, 0, 0, 0);
-    const int rho = 4 * pass + (i & 3);
-    if ((i >> 2) == gg && rho < p.R) {
-      const int s = rho / p.G, h = kvh * p.G + rho % p.G;
-      const float* qr = p.q + ((size_t)s * p.H + h) * D;
+  {
+    constexpr int QMAX = (SM::NPMAX * NT * 64 + NTHR - 1) / NTHR;  // operand slots per thread
+    const int NQ = NP * NT * 64;
+    float qv[QMAX][8];
+    bool use[QMAX];
+#pragma unroll
+    for (int i = 0; i < QMAX; i++) {
+      const int idx = i * NTHR + tid;
+      const int l = idx & 63, t = (idx >> 6) % NT, pass = (idx >> 6) / NT;
+      const int gg = l >> 4, ii = l & 15;
+      const int rho = 4 * pass + (ii & 3);
+      use[i] = idx < NQ && (ii >> 2) == gg && rho < p.R;
+      const int s = use[i] ? rho / p.G : 0, h = use[i] ? kvh * p.G + rho % p.G : 0;
+      const float* qr = p.q + ((size_t)s * p.H + h) * D + (use[i] ? qk_dim<D, QUARTER>(gg, t, 0) : 0);
+      const float4 a = *(const float4*)qr, b = *(const float4*)(qr + 4);
+      qv[i][0] = a.x; qv[i][1] = a.y; qv[i][2] = a.z; qv[i][3] = a.w;
+      qv[i][4] = b.x; qv[i][5] = b.y; qv[i][6] = b.z; qv[i][7] = b.w;
+    }
+    const int ta = tile0 < t_end ? tile0 : t_end - 1;
+    load_tile<D, DT, QUARTER>(A, ta * 32, g, n, kbase, vbase, ksb, vsb);
+    __builtin_amdgcn_sched_barrier(0);  // every load above is issued before the first wait
+#pragma unroll
+    for (int i = 0; i < QMAX; i++) {
+      const int idx = i * NTHR + tid;
+      H8 hi, lo;
 #pragma unroll
       for (int e = 0; e < 8; e++) {
-        const float x = qr[qk_dim<D, QUARTER>(gg, t, e)] * p.qscale;
-        const _Float16 hi = (_Float16)x;
-        v.h[e] = hl ? (_Float16)(x - (float)hi) : hi;
+        const float x = use[i] ? qv[i][e] * p.qscale : 0.0f;
+        const _Float16 h16 = (_Float16)x;
+        hi.h[e] = h16;
+        lo.h[e] = (_Float16)(x - (float)h16);
       }
+      const int l = idx & 63, pt = idx >> 6;   // pt = pass * NT + t
+      const int o0 = idx < NQ ? (pt * 2 + 0) * 64 + l : 2 * NQ;
+      const int o1 = idx < NQ ? (pt * 2 + 1) * 64 + l : 2 * NQ + 1;
+      qs[o0] = hi.u;
+      qs[o1] = lo.u;
     }
-    qs[idx] = v.u;
   }
   // zero this wave's P tiles (rows never written stay zero) and set corr = 1
   {
@@ -273,21 +296,25 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
   auto process = [&](const TileRegs<D, DT, QUARTER>& T, int tile) {
     const int j0 = tile * 32;
     // ---------------- K operands ----------------
-    half8 kb[2][NT];
+    // K operand for QK MFMA t of 16-slot group t2: converted just in time (plain cache) or
+    // materialized once after the read-time rotation (sink mode)
+    half8 kb[2][ROLL ? NT : 1];
+    auto kop = [&](int t2, int t) -> half8 {
+      if constexpr (ROLL) {
+        return kb[t2][t];
+      } else if constexpr (DT == KV_Q8) {
+        const uint4 u = T.kr[t2][t >> 1];
+        return (t & 1) ? q8_to_half8(u.z, u.w) : q8_to_half8(u.x, u.y);
+      } else {
+        H8 h;  // piece 0 holds MFMAs t < NT/2, piece 1 the rest, stored back to back
+        h.u = T.kr[t2][t];
+        return h.h;
+      }
+    };
 #pragma unroll
     for (int t2 = 0; t2 < 2; t2++) {
       if constexpr (!ROLL) {
-#pragma unroll
-        for (int t = 0; t < NT; t++) {
-          if constexpr (DT == KV_Q8) {
-            const uint4 u = T.kr[t2][t >> 1];
-            kb[t2][t] = (t & 1) ? q8_to_half8(u.z, u.w) : q8_to_half8(u.x, u.y);
-          } else {
-            H8 h;  // piece 0 holds MFMAs t < NT/2, piece 1 the rest, stored back to back
-            h.u = T.kr[t2][t];
-            kb[t2][t] = h.h;
-          }
-        }
+        (void)t2;
       } else {
         // read-time rotation: dims (i, i + D/2) of this lane group, at the slot's rope position
         const int P = j0 + 16 * t2 + n;
@@ -349,8 +376,9 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
           ahi.u = qs[((pass * NT + t) * 2 + 0) * 64 + lane];
           alo.u = qs[((pass * NT + t) * 2 + 1) * 64 + lane];
           const int sub = QUARTER ? (t >> 2) : 0;
-          c[sub] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi.h, kb[t2][t], c[sub], 0, 0, 0);
-          c[sub] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo.h, kb[t2][t], c[sub], 0, 0, 0);
+          const half8 kt = kop(t2, t);
+          c[sub] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi.h, kt, c[sub], 0, 0, 0);
+          c[sub] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo.h, kt, c[sub], 0, 0, 0);
         }
         float v[4];
 #pragma unroll
@@ -413,20 +441,15 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
     // ---------------- PV ----------------
-    half8 va[NB][2];
-#pragma unroll
-    for (int b = 0; b < NB; b++) {
+    auto vop = [&](int b, int par) -> half8 {
       if constexpr (DT == KV_Q8) {
-        va[b][0] = q8_to_half8(T.vr[b].x, T.vr[b].y);
-        va[b][1] = q8_to_half8(T.vr[b].z, T.vr[b].w);
+        return par ? q8_to_half8(T.vr[b].z, T.vr[b].w) : q8_to_half8(T.vr[b].x, T.vr[b].y);
       } else {
-        H8 e0, e1;
-        e0.u = T.vr[2 * b];
-        e1.u = T.vr[2 * b + 1];
-        va[b][0] = e0.h;
-        va[b][1] = e1.h;
+        H8 e;
+        e.u = T.vr[2 * b + par];
+        return e.h;
       }
-    }
+    };
 #pragma unroll
     for (int st = 0; st < NSET; st++) {
       const float cr = cl[16 * st + n];
@@ -436,8 +459,8 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
       for (int b = 0; b < NB; b++) {
         H8 pb;
         pb.u = *(const uint4*)(pl + ((size_t)(NBV > 1 ? b : 0) * RS + 16 * st + n) * 32 + 8 * g);
-        o[st][2 * b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[b][0], pb.h, o[st][2 * b], 0, 0, 0);
-        o[st][2 * b + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[b][1], pb.h, o[st][2 * b + 1], 0, 0, 0);
+        o[st][2 * b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop(b, 0), pb.h, o[st][2 * b], 0, 0, 0);
+        o[st][2 * b + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop(b, 1), pb.h, o[st][2 * b + 1], 0, 0, 0);
       }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -527,54 +550,91 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
   }
   __syncthreads();
   if (!s_last) return;
-  const float* wo = p.ws_o + (size_t)kvh * p.n_splits * p.R * D;
-  const float* wml = p.ws_ml + (size_t)kvh * p.n_splits * p.R * 2;
+  // Coherent reads of the other workgroups' partials: buffer loads with the sc1 (agent
+  // coherence) cache policy -- ordinary loads to the compiler, so a batch stays in flight.
   const int NS = p.n_splits;
-  // (1) per-split weights w[sp][row] = exp2(m_sp - M) / L into LDS
-  float* wts = (float*)smem;                   // [NS][R]
-  float* lsp = wts + NS * p.R;                 // [NS][R]
-  for (int i = tid; i < NS * p.R; i += NTHR) {
-    const float2 ml = ld_coherent2(&wml[2 * i]);
-    wts[i] = ml.x;
-    lsp[i] = ml.y;
-  }
-  __syncthreads();
-  for (int rho = tid; rho < p.R; rho += NTHR) {
-    float M = -1e30f;
-    for (int sp = 0; sp < NS; sp++) M = fmaxf(M, wts[sp * p.R + rho]);
-    float L = 0.0f;
-    for (int sp = 0; sp < NS; sp++) L += lsp[sp * p.R + rho] * exp2f(wts[sp * p.R + rho] - M);
-    const float inv = 1.0f / L;
-    for (int sp = 0; sp < NS; sp++) wts[sp * p.R + rho] = exp2f(wts[sp * p.R + rho] - M) * inv;
-  }
-  __syncthreads();
-  // (2) weighted sum of the split partials: float4 columns, TPC threads per column
-  const int C4 = p.R * D / 4;
-  const int TPC = NTHR >= C4 ? NTHR / C4 : 1;
+  const int R = p.R;
+  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.ws_o + (size_t)kvh * NS * R * D), (short)0, 0x7fffffff, 0x00020000);
+  const __amdgpu_buffer_rsrc_t mrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.ws_ml + (size_t)kvh * NS * R * 2), (short)0, 0x7fffffff, 0x00020000);
+  constexpr int kSC1 = 16;                     // cache policy: sc1
+  constexpr int MAXL = 8;                      // partial float4 loads in flight per thread
+  const int C4 = R * D / 4;
+  const int TPC = NTHR >= C4 ? NTHR / C4 : 1;  // threads per float4 column
   const int CPT = NTHR / TPC;                  // columns per pass
-  float4* red = (float4*)(lsp + NS * p.R);     // [TPC][C4] partial sums
+  float* wts = (float*)smem;                   // [NS][R] merge weights
+  float* mls = wts + NS * R;                   // [NS][R][2]
+  float4* red = (float4*)(mls + 2 * NS * R);   // [TPC][CPT] partial sums
+  // (1) (m, l) of every split -> LDS, while the first batch of partials is already in flight
+  floatx4 pre[MAXL];
+  {
+    const int c = tid % CPT, k = tid / CPT;
+    const bool act = c < C4 && k < TPC;
+#pragma unroll
+    for (int i = 0; i < MAXL; i++) {
+      const int sp = k + TPC * i;
+      pre[i] = (act && sp < NS) ? __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(
+                                      wrs, (sp * R * D + 4 * c) * 4, 0, kSC1))
+                                : floatx4{0, 0, 0, 0};
+    }
+  }
+  for (int i = tid; i < NS * R; i += NTHR) {
+    const uint2 u = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(mrs, i * 8, 0, kSC1));
+    mls[2 * i] = __uint_as_float(u.x);
+    mls[2 * i + 1] = __uint_as_float(u.y);
+  }
+  __syncthreads();
+  // (2) weights: one wave per row, lanes over splits
+  for (int rho = wave; rho < R; rho += NW) {
+    float mx = -1e30f;
+    for (int sp = lane; sp < NS; sp += 64) mx = fmaxf(mx, mls[2 * (sp * R + rho)]);
+    mx = wave_max(mx);
+    float lt = 0.0f;
+    for (int sp = lane; sp < NS; sp += 64) lt += mls[2 * (sp * R + rho) + 1] * exp2f(mls[2 * (sp * R + rho)] - mx);
+    lt = wave_sum(lt);
+    const float inv = 1.0f / lt;
+    for (int sp = lane; sp < NS; sp += 64) wts[sp * R + rho] = exp2f(mls[2 * (sp * R + rho)] - mx) * inv;
+  }
+  __syncthreads();
+  // (3) weighted sum of the partials, TPC threads per column, MAXL loads in flight per thread
   for (int c0 = 0; c0 < C4; c0 += CPT) {
     const int c = c0 + tid % CPT;
     const int k = tid / CPT;
+    const bool act = c < C4 && k < TPC;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (c < C4 && k < TPC) {
+    if (act) {
       const int rho = (4 * c) / D;
-#pragma unroll 8
-      for (int sp = k; sp < NS; sp += TPC) {
-        const float* src = wo + (size_t)sp * p.R * D + 4 * c;
-        const float2 a = ld_coherent2(src), b = ld_coherent2(src + 2);
-        const float w = wts[sp * p.R + rho];
-        acc.x += a.x * w;
-        acc.y += a.y * w;
-        acc.z += b.x * w;
-        acc.w += b.y * w;
+      for (int b0 = 0; b0 < NS; b0 += TPC * MAXL) {
+        floatx4 v[MAXL];
+        if (b0 == 0 && c0 == 0) {
+#pragma unroll
+          for (int i = 0; i < MAXL; i++) v[i] = pre[i];
+        } else {
+#pragma unroll
+          for (int i = 0; i < MAXL; i++) {
+            const int sp = b0 + k + TPC * i;
+            v[i] = sp < NS ? __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(
+                                 wrs, (sp * R * D + 4 * c) * 4, 0, kSC1))
+                           : floatx4{0, 0, 0, 0};
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < MAXL; i++) {
+          const int sp = b0 + k + TPC * i;
+          const float w = sp < NS ? wts[sp * R + rho] : 0.0f;
+          acc.x += v[i][0] * w;
+          acc.y += v[i][1] * w;
+          acc.z += v[i][2] * w;
+          acc.w += v[i][3] * w;
+        }
       }
-      red[(size_t)k * C4 + c] = acc;
+      red[(size_t)k * CPT + (c - c0)] = acc;
     }
     __syncthreads();
-    if (k == 0 && c < C4) {
+    if (act && k == 0) {
       for (int kk = 1; kk < TPC; kk++) {
-        const float4 v = red[(size_t)kk * C4 + c];
+        const float4 v = red[(size_t)kk * CPT + (c - c0)];
         acc.x += v.x;
         acc.y += v.y;
         acc.z += v.z;
@@ -666,7 +726,8 @@ static hipError_t launch_cfg(const LayerView& L, const AttnArgs& a, hipStream_t 
   // the split merge reuses the space: weights + l [NS][R] and float4 partial sums
   const size_t C4 = (size_t)p.R * D / 4;
   const size_t tpc = (size_t)64 * NW >= C4 ? (size_t)64 * NW / C4 : 1;
-  const size_t merge = (size_t)2 * sp.n_splits * p.R * 4 + tpc * C4 * 16;
+  const size_t cpt = (size_t)64 * NW / tpc;
+  const size_t merge = (size_t)3 * sp.n_splits * p.R * 4 + tpc * cpt * 16;
   smem = smem > merge ? smem : merge;
   if (smem > 160 * 1024) return hipErrorInvalidValue;
   if (smem > 64 * 1024) {
