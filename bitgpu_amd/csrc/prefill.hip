@@ -5,23 +5,32 @@
 // subgroup or workgroup per (query, head) with a serial key loop. Here prefill is a dense
 // contraction:
 //   rows      a row is a (query, head) pair; the G heads of one kv head are packed into the rows
-//             so every staged K/V byte serves G heads. A wave owns 32 rows, a workgroup 128.
-//   teams     a workgroup is 8 waves = two teams of 4. Both teams hold the same 128 rows; team 0
-//             scans the first half of the block's key range, team 1 the second half, and the two
-//             online-softmax states are merged through LDS at the end. Two waves per SIMD (one
-//             of each team) let one wave's softmax overlap the other's MFMAs, and the halves are
-//             equal so neither team idles. Blocks are launched heaviest (latest queries) first.
-//   staging   per step a team stages KT keys (64 for D=128, 32 for D=256): K row-major and V^T
-//             (the cache's transposed 32-slot tiles) into LDS as f16, double-buffered with one
-//             barrier per step; the next step's global loads are in flight while this step
-//             computes. q8 codes are dequantized (code * block scale / 127) once per workgroup
-//             on the way in; sink-mode keys are rotated at their slot position on the way in.
+//             so every staged K/V byte serves G heads. A wave owns 32 rows, a team of 4 waves 128.
+//   teams     D=128: a workgroup is 8 waves = two teams of 4. Both teams hold the same 128 rows;
+//             team 0 scans the first half of the block's key range, team 1 the second half, and
+//             the two online-softmax states are merged through LDS at the end. Two waves per
+//             SIMD (one of each team) let one wave's softmax overlap the other's MFMAs, and the
+//             halves are equal so neither team idles. D=256 keeps one team of 4 waves, each with
+//             a full SIMD's registers.
+//   items     D=128: a workgroup processes a heavy query block (late queries, long key range)
+//             and its mirror light block, so all workgroups do about the same work in one wave
+//             of the grid -- no causal tail, no dispatch gaps. D=256: one block per workgroup,
+//             heaviest first, balanced by the dispatcher.
+//   staging   per step a team stages KT keys (64 for D=128, 32 for D=256) of K (row-major, 16-byte
+//             chunks XOR-swizzled by row so the MFMA operand reads hit distinct banks) and V^T
+//             (the cache's transposed 32-slot tiles, copied as they are) into LDS as f16,
+//             double-buffered with one barrier per step. An f16 cache is copied by the gfx950
+//             direct-to-LDS loads (global_load_lds_dwordx4: no registers, no VALU); q8 codes are
+//             dequantized (code * block scale / 127) and sink-mode keys rotated at their slot
+//             position through registers, once per workgroup. Either way the next step's loads
+//             are in flight while this step computes.
 //   S^T = K Q^T  v_mfma_f32_32x32x16_f16, A = K from LDS, B = Q^T held in registers: a lane
 //             holds 16 keys of ONE row, so the softmax is lane-local plus one cross-half shuffle.
-//   softmax   base 2; masks only on steps that reach past the block's first query (causal
+//   softmax   base 2 with the hardware exp2 (results below 2^-126 flush to 0, as the f16 P
+//             operand would); masks only on steps that reach past the block's first query (causal
 //             diagonal) or the scanned range; the running max is raised only when a step's max
 //             exceeds it by more than 8 (so P <= 2^8, exact-range f16) -- most steps skip the
-//             O rescale.
+//             O rescale. The row sum accumulates the f16 P the PV product uses (v_dot2).
 //   O^T += V^T P^T  v_mfma_f32_32x32x16_f16: the S^T accumulator registers are already in the
 //             B-operand layout of P^T for the V tile's panel order, no transpose.
 // The output gate (gate_sigmoid.wgsl:13) is applied at the store.
@@ -30,11 +39,21 @@
 namespace bg {
 
 typedef _Float16 half8p __attribute__((ext_vector_type(8)));
+typedef _Float16 half2p __attribute__((ext_vector_type(2)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+// native 16-byte vector (HIP's uint4 is a struct whose copies become memcpys the optimizer
+// cannot always keep in registers)
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+__device__ inline u32x4 ldv(const void* p) { return *(const u32x4*)p; }
+__device__ inline void stv(void* p, u32x4 v) { *(u32x4*)p = v; }
+
+typedef __attribute__((address_space(3))) void* lds_vptr;
+typedef __attribute__((address_space(1))) void* glb_vptr;
 
 union PH8 {
   half8p h;
-  uint4 u;
+  u32x4 u;
+  half2p p[4];
   _Float16 e[8];
 };
 
@@ -59,28 +78,27 @@ template <int D>
 struct PfCfg {
   static constexpr int KT = D == 128 ? 64 : 32;   // keys per step
   static constexpr int NSUB = KT / 32;            // 32-key MFMA sub-tiles per step
-  static constexpr int KS = D + 8;                // staged K row stride in f16 (bank spread)
-  static constexpr int K_HALFS = KT * KS;
-  static constexpr int V_HALFS = KT * D;
-  static constexpr int BUF_HALFS = K_HALFS + V_HALFS;   // one team's buffer
+  static constexpr int CPR = D / 8;               // 16-byte chunks per K row
+  static constexpr int TILE = KT * D;             // f16 values of one staged K (or V) tile
   static constexpr int NC = D / 16;               // QK k-chunks
   static constexpr int ND = D / 32;               // output dim chunks
   static constexpr int NB = D / 32;               // q8 scale blocks per row
-  static constexpr size_t stage_bytes = (size_t)4 * BUF_HALFS * 2;          // 2 teams x 2 buffers
-  static constexpr size_t merge_bytes = (size_t)4 * 64 * (ND * 16 + 2) * 4;  // team 1's states
-  static constexpr size_t smem = stage_bytes > merge_bytes ? stage_bytes : merge_bytes;
 };
 
-// One thread's share of a step's staging: 16 dims of one key in each half of the row (the rope
-// partners i and i + D/2 sit in the same thread) and 4 V^T chunks of 8 slots (f16: 4 chunks
-// spread over the step; q8: the chunks of 4 neighbouring dims of one panel, which share the
-// 8 slot scales of one block).
+// staged K: chunk c of row r lives at chunk position r * CPR + (c ^ (r & 15))
+template <int D>
+__device__ inline int k_chunk_pos(int r, int c) { return r * PfCfg<D>::CPR + (c ^ (r & 15)); }
+
+// One thread's share of a register-staged step (q8 or sink mode): 16 dims of one key in each
+// half of the row (the rope partners i and i + D/2 sit in the same thread) and 4 V^T chunks of
+// 8 slots (f16: 4 chunks spread over the step; q8: the chunks of 4 neighbouring dims of one
+// panel, which share the 8 slot scales of one block).
 template <int D, int DT>
 struct StageRegs {
   static constexpr bool Q8 = DT == KV_Q8;
-  uint4 k[Q8 ? 2 : 4];        // q8: 16 codes per half; f16: 2 x 8 values per half
+  u32x4 k[Q8 ? 2 : 4];        // q8: 16 codes per half; f16: 2 x 8 values per half
   float ksc[Q8 ? 2 : 1];
-  uint4 v[Q8 ? 2 : 4];        // q8: 4 dims x 8 slots of codes; f16: 4 x 8 values
+  u32x4 v[Q8 ? 2 : 4];        // q8: 4 dims x 8 slots of codes; f16: 4 x 8 values
   float vsc[Q8 ? 8 : 1];      // q8: block scale of each of the 8 slots
 };
 
@@ -88,13 +106,16 @@ template <int D, int DT, bool ROLL>
 struct Stager {
   using C = PfCfg<D>;
   static constexpr int PH = D / 32;   // threads per key (16 dims per half each)
+  int tt, wt, lane;
   // K piece of this thread
-  int tt, key, cb;
+  int key, cb;
   // q8 V chunk group of this thread: dims 4*vdg .. 4*vdg+3 of panel vpanel of 32-slot tile vu
   int vu, vpanel, vdg;
 
   __device__ explicit Stager(int t) {
     tt = t;
+    wt = t >> 6;
+    lane = t & 63;
     key = t / PH;
     cb = 16 * (t % PH);
     vdg = t % (D / 4);
@@ -102,32 +123,59 @@ struct Stager {
     vu = t / D;
   }
 
-  // issue the global loads of the step whose first key is slot j0
+  // f16 cache without rotation: this wave's 4 K and 4 V chunks of 64 lanes copied straight
+  // into LDS (the step's tiles are 4 waves x 4 x 64 chunks of 16 bytes each)
+  __device__ __forceinline__ void dma(const PrefillParams& p, int kvh, int j0, _Float16* kdst, _Float16* vdst) const {
+    const LayerView& L = p.L;
+    const int cap = L.cap;
+    const __half* kg = (const __half*)L.k + (size_t)kvh * cap * D;
+    const __half* vg = (const __half*)L.v + (size_t)kvh * cap * D;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int pb = (4 * i + wt) * 64;   // first chunk position of this wave instruction
+      const int P = pb + lane;
+      const int r = P / C::CPR;
+      const int c = (P % C::CPR) ^ (r & 15);
+      const __half* src = kg + (size_t)min(j0 + r, cap - 1) * D + c * 8;  // past the end: masked keys
+      __builtin_amdgcn_global_load_lds((glb_vptr)src, (lds_vptr)(kdst + pb * 8), 16, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int pb = (4 * i + wt) * 64;
+      const int P = pb + lane;
+      const int u = P / (4 * D);        // 32-slot tile of the chunk (4*D chunks per tile)
+      const int tu = min((j0 >> 5) + u, cap / 32 - 1);
+      const __half* src = vg + (size_t)tu * 32 * D + (size_t)(P % (4 * D)) * 8;
+      __builtin_amdgcn_global_load_lds((glb_vptr)src, (lds_vptr)(vdst + pb * 8), 16, 0, 0);
+    }
+  }
+
+  // register staging: issue the global loads of the step whose first key is slot j0
   __device__ __forceinline__ void load(StageRegs<D, DT>& R, const PrefillParams& p, int kvh, int j0) const {
     const LayerView& L = p.L;
     const int cap = L.cap;
     const int slot = min(j0 + key, cap - 1);  // past the end: a valid row whose keys are masked
     if constexpr (DT == KV_Q8) {
       const int8_t* kr = (const int8_t*)L.k + ((size_t)kvh * cap + slot) * D;
-      R.k[0] = *(const uint4*)(kr + cb);
-      R.k[1] = *(const uint4*)(kr + cb + D / 2);
+      R.k[0] = ldv(kr + cb);
+      R.k[1] = ldv(kr + cb + D / 2);
       const float* ks = L.ks + ((size_t)kvh * cap + slot) * C::NB;
       R.ksc[0] = ks[cb / 32];
       R.ksc[1] = ks[(cb + D / 2) / 32];
       const int t32 = min((j0 >> 5) + vu, cap / 32 - 1);
       const int8_t* vt = (const int8_t*)L.v + ((size_t)kvh * cap + (size_t)t32 * 32) * D +
                          ((size_t)vpanel * D + 4 * vdg) * 8;
-      R.v[0] = *(const uint4*)vt;
-      R.v[1] = *(const uint4*)(vt + 16);
+      R.v[0] = ldv(vt);
+      R.v[1] = ldv(vt + 16);
       const float* vs = L.vs + ((size_t)kvh * cap + (size_t)t32 * 32) * C::NB + (4 * vdg) / 32;
 #pragma unroll
       for (int e = 0; e < 8; e++) R.vsc[e] = vs[(size_t)tile_slot(vpanel, e) * C::NB];
     } else {
       const __half* kr = (const __half*)L.k + ((size_t)kvh * cap + slot) * D;
-      R.k[0] = *(const uint4*)(kr + cb);
-      R.k[1] = *(const uint4*)(kr + cb + 8);
-      R.k[2] = *(const uint4*)(kr + cb + D / 2);
-      R.k[3] = *(const uint4*)(kr + cb + D / 2 + 8);
+      R.k[0] = ldv(kr + cb);
+      R.k[1] = ldv(kr + cb + 8);
+      R.k[2] = ldv(kr + cb + D / 2);
+      R.k[3] = ldv(kr + cb + D / 2 + 8);
       // V^T: the step's KT slots are KT * D contiguous values; chunk = tt + 256 i
       const int t32 = j0 >> 5;
 #pragma unroll
@@ -136,19 +184,20 @@ struct Stager {
         const int u = c / (4 * D);                  // 32-slot tile of the chunk
         const int tu = min(t32 + u, cap / 32 - 1);
         const __half* vt = (const __half*)L.v + ((size_t)kvh * cap + (size_t)tu * 32) * D;
-        R.v[i] = *(const uint4*)(vt + (size_t)(c % (4 * D)) * 8);
+        R.v[i] = ldv(vt + (size_t)(c % (4 * D)) * 8);
       }
     }
   }
 
-  // convert (dequantize / rotate) and write into one team buffer; j0 = the staged step's first key
+  // register staging: convert (dequantize / rotate) and write into one buffer; j0 = the staged
+  // step's first key
   __device__ __forceinline__ void store(const StageRegs<D, DT>& R, const PrefillParams& p, int j0, _Float16* kb,
                                         _Float16* vb) const {
     float a[16], b[16];  // the two halves of this thread's 16-dim K piece
     if constexpr (DT == KV_Q8) {
       const float sa = R.ksc[0] * (1.0f / 127.0f), sb = R.ksc[1] * (1.0f / 127.0f);
-      const uint32_t wa[4] = {R.k[0].x, R.k[0].y, R.k[0].z, R.k[0].w};
-      const uint32_t wb[4] = {R.k[1].x, R.k[1].y, R.k[1].z, R.k[1].w};
+      const uint32_t wa[4] = {R.k[0][0], R.k[0][1], R.k[0][2], R.k[0][3]};
+      const uint32_t wb[4] = {R.k[1][0], R.k[1][1], R.k[1][2], R.k[1][3]};
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const uint32_t ua = wa[i] ^ 0x80808080u, ub = wb[i] ^ 0x80808080u;  // biased: u = c + 128
@@ -194,25 +243,26 @@ struct Stager {
         }
       }
     }
+    const int ca = cb / 8, cbb = (cb + D / 2) / 8;  // first chunk of each half
     if constexpr (DT == KV_Q8 || ROLL) {
       PH8 o;
 #pragma unroll
       for (int i = 0; i < 2; i++) {
 #pragma unroll
         for (int e = 0; e < 8; e++) o.e[e] = (_Float16)a[8 * i + e];
-        *(uint4*)(kb + key * C::KS + cb + 8 * i) = o.u;
+        stv(kb + k_chunk_pos<D>(key, ca + i) * 8, o.u);
 #pragma unroll
         for (int e = 0; e < 8; e++) o.e[e] = (_Float16)b[8 * i + e];
-        *(uint4*)(kb + key * C::KS + cb + D / 2 + 8 * i) = o.u;
+        stv(kb + k_chunk_pos<D>(key, cbb + i) * 8, o.u);
       }
     } else {
-      *(uint4*)(kb + key * C::KS + cb) = R.k[0];
-      *(uint4*)(kb + key * C::KS + cb + 8) = R.k[1];
-      *(uint4*)(kb + key * C::KS + cb + D / 2) = R.k[2];
-      *(uint4*)(kb + key * C::KS + cb + D / 2 + 8) = R.k[3];
+      stv(kb + k_chunk_pos<D>(key, ca) * 8, R.k[0]);
+      stv(kb + k_chunk_pos<D>(key, ca + 1) * 8, R.k[1]);
+      stv(kb + k_chunk_pos<D>(key, cbb) * 8, R.k[2]);
+      stv(kb + k_chunk_pos<D>(key, cbb + 1) * 8, R.k[3]);
     }
     if constexpr (DT == KV_Q8) {
-      const uint32_t w[8] = {R.v[0].x, R.v[0].y, R.v[0].z, R.v[0].w, R.v[1].x, R.v[1].y, R.v[1].z, R.v[1].w};
+      const uint32_t w[8] = {R.v[0][0], R.v[0][1], R.v[0][2], R.v[0][3], R.v[1][0], R.v[1][1], R.v[1][2], R.v[1][3]};
       float sv[8], nb[8];
 #pragma unroll
       for (int e = 0; e < 8; e++) {
@@ -227,11 +277,11 @@ struct Stager {
           const uint32_t u = w[2 * i + (e >> 2)] ^ 0x80808080u;
           o.e[e] = (_Float16)fmaf((float)((u >> (8 * (e & 3))) & 0xffu), sv[e], nb[e]);
         }
-        *(uint4*)(vb + ((size_t)(vu * 4 + vpanel) * D + 4 * vdg + i) * 8) = o.u;
+        stv(vb + ((size_t)(vu * 4 + vpanel) * D + 4 * vdg + i) * 8, o.u);
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < 4; i++) *(uint4*)(vb + (size_t)(tt + 256 * i) * 8) = R.v[i];
+      for (int i = 0; i < 4; i++) stv(vb + (size_t)(tt + 256 * i) * 8, R.v[i]);
     }
   }
 };
@@ -239,9 +289,14 @@ struct Stager {
 template <int D, int DT, bool ROLL, int TEAMS>
 __global__ __launch_bounds__(256 * TEAMS) void prefill_kernel(PrefillParams p) {
   using C = PfCfg<D>;
-  constexpr int KT = C::KT, NSUB = C::NSUB, NC = C::NC, ND = C::ND, KS = C::KS;
-  extern __shared__ __align__(16) unsigned char smem_raw[];
-  _Float16* smem = (_Float16*)smem_raw;
+  constexpr int KT = C::KT, NSUB = C::NSUB, NC = C::NC, ND = C::ND, TILE = C::TILE;
+  constexpr bool DMA = DT == KV_F16 && !ROLL;
+  // Double buffers as four distinct arrays, [team][tile] each: the compiler then knows a DMA
+  // into one buffer cannot alias the reads of the other, and adds no waits between them.
+  __shared__ __align__(16) _Float16 lk0[TEAMS * TILE];
+  __shared__ __align__(16) _Float16 lk1[TEAMS * TILE];
+  __shared__ __align__(16) _Float16 lv0[TEAMS * TILE];
+  __shared__ __align__(16) _Float16 lv1[TEAMS * TILE];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
@@ -249,75 +304,104 @@ __global__ __launch_bounds__(256 * TEAMS) void prefill_kernel(PrefillParams p) {
   const int tt = tid & 255;  // thread index within the team
   const int g2 = lane >> 5, n = lane & 31;
   const int KV = p.L.kv_heads;
-  const int kvh = blockIdx.x % KV;
-  const int qb = p.n_qblocks - 1 - (int)(blockIdx.x / KV);  // heaviest (latest) blocks first
-  const int s0 = qb * p.QB;
-
-  // this lane's row
-  const int r = wt * 32 + n;
-  const int qi = s0 + r / p.G;
-  const int h = kvh * p.G + r % p.G;
-  const bool row_ok = r < p.QB * p.G && qi < p.S;
-  const int limit = p.pos_base + qi;
-
-  // key range of the block, split into two equal halves with two teams (team 1 takes the
-  // larger one)
-  const int last_q = min(s0 + p.QB, p.S) - 1;
-  const int n_scan = p.n_scan_fixed > 0 ? p.n_scan_fixed : p.pos_base + last_q + 1;
-  const int T = (n_scan + KT - 1) / KT;
-  const int T0 = TEAMS == 2 ? T / 2 : 0;
-  const int my_first = team ? T0 : 0;
-  const int my_count = team || TEAMS == 1 ? T - T0 : T0;
-  const int steps = T - T0;
-  // the earliest key index any row of the block masks (causal diagonal or scan end)
-  const int mask_from = min(min(p.pos_base + s0 + 1, n_scan), p.phys_limit);
-
-  _Float16* const tbuf = smem + (size_t)(team * 2) * C::BUF_HALFS;  // this team's 2 buffers
-
-  const Stager<D, DT, ROLL> stg(tt);
-  // The staging is branch-free: a team past its last step re-stages a valid (clamped) tile into
-  // the buffer nobody reads this step, so the registers stay registers and loads stay counted.
-  const int t_last = T - 1;
-  {
-    StageRegs<D, DT> R;
-    const int j0 = min(my_first, t_last) * KT;
-    stg.load(R, p, kvh, j0);
-    stg.store(R, p, j0, tbuf, tbuf + C::K_HALFS);
-  }
-
-  // Q^T operand: dims 16c + 8*g2 + [0..8), pre-scaled by scale*log2(e)
-  half8p qf[NC];
-  {
-    const float* qr = p.q + ((size_t)(row_ok ? qi : 0) * p.H + (row_ok ? h : 0)) * D;
-#pragma unroll
-    for (int c = 0; c < NC; c++) {
-      const float4 a = *(const float4*)(qr + 16 * c + 8 * g2);
-      const float4 b = *(const float4*)(qr + 16 * c + 8 * g2 + 4);
-      const float sc = row_ok ? p.qscale : 0.0f;
-      qf[c] = half8p{(_Float16)(a.x * sc), (_Float16)(a.y * sc), (_Float16)(a.z * sc), (_Float16)(a.w * sc),
-                     (_Float16)(b.x * sc), (_Float16)(b.y * sc), (_Float16)(b.z * sc), (_Float16)(b.w * sc)};
-    }
-  }
-
-  floatx16 o[ND];
-#pragma unroll
-  for (int i = 0; i < ND; i++)
-#pragma unroll
-    for (int e = 0; e < 16; e++) o[i][e] = 0.0f;
-  float m = -1e30f, lsum = 0.0f;
   const Ring ring = p.L.ring;
-  __syncthreads();
+  _Float16* const k0 = lk0 + team * TILE;
+  _Float16* const k1 = lk1 + team * TILE;
+  _Float16* const v0 = lv0 + team * TILE;
+  _Float16* const v1 = lv1 + team * TILE;
+  const Stager<D, DT, ROLL> stg(tt);
+  const int r = wt * 32 + n;  // this lane's row within the block
 
-  for (int s = 0; s < steps; s++) {
-    StageRegs<D, DT> R;
-    const int jn = min(my_first + s + 1, t_last) * KT;
-    stg.load(R, p, kvh, jn);
+  // Work items are (query block, kv head) pairs ordered heaviest (latest queries) first. With
+  // two teams (one workgroup per CU) the workgroup takes item blockIdx.x and its mirror
+  // n_items-1-blockIdx.x, so every workgroup scans about the same number of keys and the grid
+  // is one wave of workgroups; with one team the dispatcher balances one item per workgroup.
+  constexpr int ITEMS = TEAMS == 2 ? 2 : 1;
+  const int n_items = p.n_qblocks * KV;
+  for (int it = 0; it < ITEMS; it++) {
+    const int item = it == 0 ? (int)blockIdx.x : n_items - 1 - (int)blockIdx.x;
+    if (it == 1 && item <= (int)blockIdx.x) break;  // odd count: the middle workgroup has one
+    const int kvh = item % KV;
+    const int qb = p.n_qblocks - 1 - item / KV;
+    const int s0 = qb * p.QB;
 
-    if (s < my_count) {
-      const int j0 = (my_first + s) * KT;
-      const _Float16* kb = tbuf + (size_t)(s & 1) * C::BUF_HALFS;
-      const _Float16* vb = kb + C::K_HALFS;
-      // ---------------- S^T = K Q^T ----------------
+    const int qi = s0 + r / p.G;
+    const int h = kvh * p.G + r % p.G;
+    const bool row_ok = r < p.QB * p.G && qi < p.S;
+    const int limit = p.pos_base + qi;
+
+    // key range of the block, split into two equal halves with two teams (team 1 takes the
+    // larger one)
+    const int last_q = min(s0 + p.QB, p.S) - 1;
+    const int n_scan = p.n_scan_fixed > 0 ? p.n_scan_fixed : p.pos_base + last_q + 1;
+    const int T = (n_scan + KT - 1) / KT;
+    const int T0 = TEAMS == 2 ? T / 2 : 0;
+    const int my_first = team ? T0 : 0;
+    const int my_count = team || TEAMS == 1 ? T - T0 : T0;
+    const int steps = T - T0;
+    const int t_last = T - 1;
+    // the earliest key index any row of the block masks (causal diagonal or scan end)
+    const int mask_from = min(min(p.pos_base + s0 + 1, n_scan), p.phys_limit);
+
+    // ---------------- prologue: Q gather and the first tile, loads issued together ----------------
+    float4 qraw[2 * NC];
+    {
+      const float* qr = p.q + ((size_t)(row_ok ? qi : 0) * p.H + (row_ok ? h : 0)) * D;
+#pragma unroll
+      for (int c = 0; c < NC; c++) {
+        qraw[2 * c] = *(const float4*)(qr + 16 * c + 8 * g2);
+        qraw[2 * c + 1] = *(const float4*)(qr + 16 * c + 8 * g2 + 4);
+      }
+    }
+    // A team past its last step re-stages a valid (clamped) tile into the buffer nobody reads
+    // that step: the staging has no branches, so loads stay counted and registers registers.
+    const int j00 = min(my_first, t_last) * KT;
+    StageRegs<D, DT> R0;
+    if constexpr (DMA) {
+      stg.dma(p, kvh, j00, k0, v0);
+    } else {
+      stg.load(R0, p, kvh, j00);
+    }
+    // Q^T operand: dims 16c + 8*g2 + [0..8), pre-scaled by scale*log2(e)
+    half8p qf[NC];
+    {
+      const float sc = row_ok ? p.qscale : 0.0f;
+#pragma unroll
+      for (int c = 0; c < NC; c++) {
+        const float4 a = qraw[2 * c], b = qraw[2 * c + 1];
+        qf[c] = half8p{(_Float16)(a.x * sc), (_Float16)(a.y * sc), (_Float16)(a.z * sc), (_Float16)(a.w * sc),
+                       (_Float16)(b.x * sc), (_Float16)(b.y * sc), (_Float16)(b.z * sc), (_Float16)(b.w * sc)};
+      }
+    }
+    if constexpr (!DMA) stg.store(R0, p, j00, k0, v0);
+
+    floatx16 o[ND];
+#pragma unroll
+    for (int i = 0; i < ND; i++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) o[i][e] = 0.0f;
+    float m = -1e30f, lsum = 0.0f;
+    if constexpr (DMA) __builtin_amdgcn_s_waitcnt(0xf70);  // vmcnt(0): this wave's copies landed
+    __syncthreads();
+
+    // ---------------- one step: stage step s+1 into (kn, vn), compute step s from (kc, vc) ----------------
+    auto step = [&](int s, const _Float16* kc, const _Float16* vc, _Float16* kn, _Float16* vn) {
+      const int jn = min(my_first + s + 1, t_last) * KT;
+      StageRegs<D, DT> R;
+      if constexpr (DMA) {
+        stg.dma(p, kvh, jn, kn, vn);
+      } else {
+        stg.load(R, p, kvh, jn);
+        // the loads above stay ahead of the compute (left alone, the compiler sinks them to
+        // their use after it and every step waits for global memory)
+        __builtin_amdgcn_sched_barrier(0);
+      }
+
+      // a team past its last step computes on a fully masked tile (no branch around the
+      // compute, which would let the loads above sink)
+      const bool live = s < my_count;
+      const int j0 = (my_first + (live ? s : 0)) * KT;
+      // S^T = K Q^T
       floatx16 sacc[NSUB];
 #pragma unroll
       for (int u = 0; u < NSUB; u++)
@@ -328,13 +412,13 @@ __global__ __launch_bounds__(256 * TEAMS) void prefill_kernel(PrefillParams p) {
 #pragma unroll
         for (int u = 0; u < NSUB; u++) {
           PH8 a;
-          a.u = *(const uint4*)(kb + (u * 32 + n) * KS + 16 * c + 8 * g2);
+          a.u = ldv(kc + k_chunk_pos<D>(u * 32 + n, 2 * c + g2) * 8);
           sacc[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a.h, qf[c], sacc[u], 0, 0, 0);
         }
-      // ---------------- mask + online softmax (row = this lane's n) ----------------
+      // mask + online softmax (row = this lane's n)
       float x[NSUB][16];
       float mt = -INFINITY;
-      if (ROLL || j0 + KT > mask_from) {
+      if (ROLL || !live || j0 + KT > mask_from) {
 #pragma unroll
         for (int u = 0; u < NSUB; u++)
 #pragma unroll
@@ -342,8 +426,8 @@ __global__ __launch_bounds__(256 * TEAMS) void prefill_kernel(PrefillParams p) {
 #pragma unroll
             for (int e = 0; e < 4; e++) {
               const int P = j0 + 32 * u + 8 * k + 4 * g2 + e;
-              const int Lg = ring.logical(P);
-              const bool ok = P < n_scan && P < p.phys_limit && Lg <= limit;
+              const int Lg = ROLL ? ring.logical(P) : P;
+              const bool ok = live && P < n_scan && P < p.phys_limit && Lg <= limit;
               const float v = ok ? sacc[u][4 * k + e] : -INFINITY;
               x[u][4 * k + e] = v;
               mt = fmaxf(mt, v);
@@ -362,99 +446,104 @@ __global__ __launch_bounds__(256 * TEAMS) void prefill_kernel(PrefillParams p) {
       const bool grow = mt > m + 8.0f;
       if (__any(grow)) {
         const float mn = grow ? mt : m;
-        const float corr = exp2f(m - mn);
+        const float corr = __builtin_amdgcn_exp2f(m - mn);
         m = mn;
         lsum *= corr;
 #pragma unroll
         for (int i = 0; i < ND; i++) o[i] *= corr;
       }
-      float ps = 0.0f;
-#pragma unroll
-      for (int u = 0; u < NSUB; u++)
-#pragma unroll
-        for (int e = 0; e < 16; e++) {
-          x[u][e] = exp2f(x[u][e] - m);
-          ps += x[u][e];
-        }
-      lsum += ps;
-      // ---------------- O^T += V^T P^T ----------------
+      // P = exp2(S - m) as the f16 B operand of P^T; O^T += V^T P^T
+      const half2p ones = {(_Float16)1.0f, (_Float16)1.0f};
 #pragma unroll
       for (int u = 0; u < NSUB; u++)
 #pragma unroll
         for (int t = 0; t < 2; t++) {
-          half8p pb;
+          PH8 pb;
 #pragma unroll
           for (int e = 0; e < 4; e++) {
-            pb[e] = (_Float16)x[u][8 * t + e];
-            pb[4 + e] = (_Float16)x[u][8 * t + 4 + e];
+            pb.e[e] = (_Float16)__builtin_amdgcn_exp2f(x[u][8 * t + e] - m);
+            pb.e[4 + e] = (_Float16)__builtin_amdgcn_exp2f(x[u][8 * t + 4 + e] - m);
           }
+#pragma unroll
+          for (int i = 0; i < 4; i++) lsum = __builtin_amdgcn_fdot2(pb.p[i], ones, lsum, false);
           const int pnl = 2 * t + g2;
 #pragma unroll
           for (int dc = 0; dc < ND; dc++) {
             PH8 a;
-            a.u = *(const uint4*)(vb + ((size_t)(u * 4 + pnl) * D + 32 * dc + n) * 8);
-            o[dc] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a.h, pb, o[dc], 0, 0, 0);
+            a.u = ldv(vc + ((size_t)(u * 4 + pnl) * D + 32 * dc + n) * 8);
+            o[dc] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a.h, pb.h, o[dc], 0, 0, 0);
           }
         }
-    }
 
-    {
-      _Float16* kb = tbuf + (size_t)((s + 1) & 1) * C::BUF_HALFS;
-      stg.store(R, p, jn, kb, kb + C::K_HALFS);
-    }
-    __syncthreads();
-  }
-
-  // ---------------- merge the two teams' states ----------------
-  float* ms = (float*)smem_raw;  // [wt][ND*16 + 2][lane]
-  constexpr int SL = ND * 16 + 2;
-  if (TEAMS == 2 && team == 1) {
-    float* w = ms + (size_t)wt * SL * 64 + lane;
-#pragma unroll
-    for (int dc = 0; dc < ND; dc++)
-#pragma unroll
-      for (int e = 0; e < 16; e++) w[(dc * 16 + e) * 64] = o[dc][e];
-    w[(ND * 16) * 64] = m;
-    w[(ND * 16 + 1) * 64] = lsum;
-  }
-  if constexpr (TEAMS == 2) {
-    __syncthreads();
-    if (team == 1) return;
-    const float* w = ms + (size_t)wt * SL * 64 + lane;
-    const float m1 = w[(ND * 16) * 64], l1 = w[(ND * 16 + 1) * 64];
-    const float M = fmaxf(m, m1);
-    const float a0 = exp2f(m - M), a1 = exp2f(m1 - M);
-#pragma unroll
-    for (int dc = 0; dc < ND; dc++)
-#pragma unroll
-      for (int e = 0; e < 16; e++) o[dc][e] = o[dc][e] * a0 + w[(dc * 16 + e) * 64] * a1;
-    lsum = lsum * a0 + l1 * a1;
-  }
-  // ---------------- store ----------------
-  lsum += __shfl_xor(lsum, 32, 64);
-  if (!row_ok) return;
-  const float inv = 1.0f / lsum;
-  float* orow = p.out + ((size_t)qi * p.H + h) * D;
-  const float* grow_ = p.gate ? p.gate + ((size_t)qi * p.H + h) * p.gate_stride : nullptr;
-#pragma unroll
-  for (int dc = 0; dc < ND; dc++)
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-      const int d = 32 * dc + 8 * k + 4 * g2;
-      float4 v;
-      v.x = o[dc][4 * k + 0] * inv;
-      v.y = o[dc][4 * k + 1] * inv;
-      v.z = o[dc][4 * k + 2] * inv;
-      v.w = o[dc][4 * k + 3] * inv;
-      if (grow_) {
-        // gate_sigmoid.wgsl:13 form: x / (1 + exp(-g))
-        v.x = (o[dc][4 * k + 0] / lsum) / (1.0f + expf(-grow_[d + 0]));
-        v.y = (o[dc][4 * k + 1] / lsum) / (1.0f + expf(-grow_[d + 1]));
-        v.z = (o[dc][4 * k + 2] / lsum) / (1.0f + expf(-grow_[d + 2]));
-        v.w = (o[dc][4 * k + 3] / lsum) / (1.0f + expf(-grow_[d + 3]));
+      if constexpr (DMA) {
+        __builtin_amdgcn_s_waitcnt(0xf70);  // vmcnt(0): this wave's copies of step s+1 landed
+      } else {
+        stg.store(R, p, jn, kn, vn);
       }
-      *(float4*)(orow + d) = v;
+      __syncthreads();
+    };
+
+    // ---------------- main loop, two steps per turn so the buffers are fixed arrays ----------------
+    for (int s = 0; s < steps; s += 2) {
+      step(s, k0, v0, k1, v1);
+      if (s + 1 < steps) step(s + 1, k1, v1, k0, v0);
     }
+
+    // ---------------- merge the two teams' states ----------------
+    if constexpr (TEAMS == 2) {
+      // team 1's O (64 floats a lane) in lk0|lk1, its m and l in lv0: [wt][slot][lane]
+      float* mo = (float*)(wt < 2 ? lk0 : lk1) + (size_t)(wt & 1) * ND * 16 * 64 + lane;
+      float* ml = (float*)lv0 + (size_t)wt * 2 * 64 + lane;
+      if (team == 1) {
+#pragma unroll
+        for (int dc = 0; dc < ND; dc++)
+#pragma unroll
+          for (int e = 0; e < 16; e++) mo[(dc * 16 + e) * 64] = o[dc][e];
+        ml[0] = m;
+        ml[64] = lsum;
+      }
+      __syncthreads();
+      if (team == 0) {
+        const float m1 = ml[0], l1 = ml[64];
+        const float M = fmaxf(m, m1);
+        const float a0 = exp2f(m - M), a1 = exp2f(m1 - M);
+#pragma unroll
+        for (int dc = 0; dc < ND; dc++)
+#pragma unroll
+          for (int e = 0; e < 16; e++) o[dc][e] = o[dc][e] * a0 + mo[(dc * 16 + e) * 64] * a1;
+        lsum = lsum * a0 + l1 * a1;
+      }
+    }
+    // ---------------- store ----------------
+    if (team == 0) {
+      lsum += __shfl_xor(lsum, 32, 64);
+      if (row_ok) {
+        const float inv = 1.0f / lsum;
+        float* orow = p.out + ((size_t)qi * p.H + h) * D;
+        const float* grow_ = p.gate ? p.gate + ((size_t)qi * p.H + h) * p.gate_stride : nullptr;
+#pragma unroll
+        for (int dc = 0; dc < ND; dc++)
+#pragma unroll
+          for (int k = 0; k < 4; k++) {
+            const int d = 32 * dc + 8 * k + 4 * g2;
+            float4 v;
+            v.x = o[dc][4 * k + 0] * inv;
+            v.y = o[dc][4 * k + 1] * inv;
+            v.z = o[dc][4 * k + 2] * inv;
+            v.w = o[dc][4 * k + 3] * inv;
+            if (grow_) {
+              // gate_sigmoid.wgsl:13 form: x / (1 + exp(-g))
+              v.x = (o[dc][4 * k + 0] / lsum) / (1.0f + expf(-grow_[d + 0]));
+              v.y = (o[dc][4 * k + 1] / lsum) / (1.0f + expf(-grow_[d + 1]));
+              v.z = (o[dc][4 * k + 2] / lsum) / (1.0f + expf(-grow_[d + 2]));
+              v.w = (o[dc][4 * k + 3] / lsum) / (1.0f + expf(-grow_[d + 3]));
+            }
+            *(float4*)(orow + d) = v;
+          }
+      }
+    }
+    __syncthreads();  // the merge area is the next item's staging buffers
+  }
 }
 
 bool prefill_supported(const LayerView& L, int S, int H) {
@@ -469,16 +558,9 @@ bool prefill_supported(const LayerView& L, int S, int H) {
 template <int D, int DT, bool ROLL>
 static hipError_t launch_pf(const PrefillParams& p, hipStream_t st) {
   constexpr int TEAMS = D == 128 ? 2 : 1;
-  constexpr size_t smem = TEAMS == 2 ? PfCfg<D>::smem : PfCfg<D>::stage_bytes / 2;
-  static bool attr_set = false;  // per instantiation
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)prefill_kernel<D, DT, ROLL, TEAMS>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
-  hipLaunchKernelGGL((prefill_kernel<D, DT, ROLL, TEAMS>), dim3(p.n_qblocks * p.L.kv_heads), dim3(256 * TEAMS),
-                     smem, st, p);
+  const int n_items = p.n_qblocks * p.L.kv_heads;
+  const int n_wg = TEAMS == 2 ? (n_items + 1) / 2 : n_items;
+  hipLaunchKernelGGL((prefill_kernel<D, DT, ROLL, TEAMS>), dim3(n_wg), dim3(256 * TEAMS), 0, st, p);
   return hipGetLastError();
 }
 
