@@ -34,6 +34,8 @@
 //   O^T += V^T P^T  v_mfma_f32_32x32x16_f16: the S^T accumulator registers are already in the
 //             B-operand layout of P^T for the V tile's panel order, no transpose.
 // The output gate (gate_sigmoid.wgsl:13) is applied at the store.
+#include <type_traits>
+
 #include "bg_kernels.h"
 
 namespace bg {
@@ -324,9 +326,13 @@ __global__ __launch_bounds__(256 * TEAMS) void prefill_kernel(PrefillParams p) {
     const int kvh = item % KV;
     const int qb = p.n_qblocks - 1 - item / KV;
     const int s0 = qb * p.QB;
+    // G is laundered per item: row index math that depends only on the lane would otherwise be
+    // hoisted out of the item loop and held in registers through the whole step loop
+    int G = p.G;
+    asm volatile("" : "+s"(G));
 
-    const int qi = s0 + r / p.G;
-    const int h = kvh * p.G + r % p.G;
+    const int qi = s0 + r / G;
+    const int h = kvh * G + r % G;
     const bool row_ok = r < p.QB * p.G && qi < p.S;
     const int limit = p.pos_base + qi;
 
@@ -517,7 +523,58 @@ __global__ __launch_bounds__(256 * TEAMS) void prefill_kernel(PrefillParams p) {
     // ---------------- store ----------------
     if (team == 0) {
       lsum += __shfl_xor(lsum, 32, 64);
-      if (row_ok) {
+      if constexpr (TEAMS == 2) {
+        // through this wave's own merge region: rows written swizzled, read back and stored as
+        // contiguous 512-byte rows (the register layout scatters 16 bytes per row)
+        float4* rows = (float4*)((float*)(wt < 2 ? lk0 : lk1) + (size_t)(wt & 1) * ND * 16 * 64);
+        // lane and G laundered: the swizzled addresses below are computed here, not at the
+        // kernel start (where they would be held, or spilled, through the step loop)
+        int ln = lane, Ge = G;
+        asm volatile("" : "+v"(ln), "+s"(Ge));
+        const int en = ln & 31, eg = ln >> 5;
+        const float inv = 1.0f / lsum;
+        if (p.gate) {  // the gate divides o / l first (gate_sigmoid.wgsl:13 on the normalized row)
+#pragma unroll
+          for (int dc = 0; dc < ND; dc++)
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+              rows[en * 32 + ((8 * dc + 2 * k + eg) ^ en)] =
+                  make_float4(o[dc][4 * k] / lsum, o[dc][4 * k + 1] / lsum, o[dc][4 * k + 2] / lsum, o[dc][4 * k + 3] / lsum);
+        } else {
+#pragma unroll
+          for (int dc = 0; dc < ND; dc++)
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+              rows[en * 32 + ((8 * dc + 2 * k + eg) ^ en)] =
+                  make_float4(o[dc][4 * k] * inv, o[dc][4 * k + 1] * inv, o[dc][4 * k + 2] * inv, o[dc][4 * k + 3] * inv);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const int cl = en;
+        auto emit = [&](auto gated) {
+#pragma unroll
+          for (int i = 0; i < 16; i++) {
+            const int rl = 2 * i + eg;                 // row within the wave
+            const int rb = wt * 32 + rl;               // row within the block
+            const int qq = s0 + rb / Ge, hh = kvh * Ge + rb % Ge;
+            float4 v = rows[rl * 32 + (cl ^ (rl & 31))];
+            if (rb < p.QB * Ge && qq < p.S) {
+              if constexpr (decltype(gated)::value) {
+                // gate_sigmoid.wgsl:13 form: x / (1 + exp(-g))
+                const float4 gv = *(const float4*)(p.gate + ((size_t)qq * p.H + hh) * p.gate_stride + 4 * cl);
+                v.x = v.x / (1.0f + expf(-gv.x));
+                v.y = v.y / (1.0f + expf(-gv.y));
+                v.z = v.z / (1.0f + expf(-gv.z));
+                v.w = v.w / (1.0f + expf(-gv.w));
+              }
+              *(float4*)(p.out + ((size_t)qq * p.H + hh) * D + 4 * cl) = v;
+            }
+          }
+        };
+        if (p.gate) emit(std::true_type{});
+        else emit(std::false_type{});
+      } else if (row_ok) {
         const float inv = 1.0f / lsum;
         float* orow = p.out + ((size_t)qi * p.H + h) * D;
         const float* grow_ = p.gate ? p.gate + ((size_t)qi * p.H + h) * p.gate_stride : nullptr;
