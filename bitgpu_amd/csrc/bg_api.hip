@@ -391,7 +391,11 @@ int32_t bg_qkv_prologue(bg_kv_cache* c, int32_t layer, const float* q, int32_t q
 
 static int32_t ensure_workspace(bg_kv_cache* c, int S, int H) {
   size_t counters = 0;
-  const size_t need = bg::decode_workspace_floats(view(c, 0), S, H, c->num_cus, &counters);
+  size_t need = bg::decode_workspace_floats(view(c, 0), S, H, c->num_cus, &counters);
+  if (c->dtype == BG_KV_F32) {
+    const size_t f = bg::f32_workspace_floats(view(c, 0), S, H);
+    need = f > need ? f : need;
+  }
   if (need <= c->ws_floats && counters <= c->ws_counters) return BG_OK;
   if (c->ws) (void)hipFree(c->ws);
   if (c->ws_count) (void)hipFree(c->ws_count);
@@ -416,7 +420,7 @@ static int32_t ensure_workspace(bg_kv_cache* c, int S, int H) {
 
 int32_t bg_attention_reserve(bg_kv_cache* c, int32_t S, int32_t H) {
   if (!c || S < 1 || H < 1 || H % c->kv_heads) return fail(BG_E_INVALID, "bg_attention_reserve: bad arguments");
-  if (!bg::decode_supported(view(c, 0), S, H)) return BG_OK;
+  if (!bg::decode_supported(view(c, 0), S, H) && !bg::f32_split_supported(view(c, 0), S, H)) return BG_OK;
   return ensure_workspace(c, S, H);
 }
 
@@ -454,7 +458,14 @@ int32_t bg_attention(bg_kv_cache* c, int32_t layer, const float* q, int32_t S, i
   a.num_cus = c->num_cus;
   hipStream_t st = (hipStream_t)stream;
   hipError_t e;
-  if (c->dtype == BG_KV_F32) {
+  if (c->dtype == BG_KV_F32 && bg::f32_split_supported(L, S, H)) {
+    int32_t rc = ensure_workspace(c, S, H);
+    if (rc != BG_OK) return rc;
+    a.ws_o = c->ws;
+    a.ws_count = c->ws_count;
+    a.ws_floats = c->ws_floats;
+    e = bg::launch_attention_f32_split(L, a, st);
+  } else if (c->dtype == BG_KV_F32) {
     e = bg::launch_attention_f32(L, a, st);
   } else if (bg::decode_supported(L, S, H)) {
     int32_t rc = ensure_workspace(c, S, H);

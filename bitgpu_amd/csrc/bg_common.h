@@ -97,4 +97,25 @@ __device__ inline float group16_sum(float v) {
   return v;
 }
 
+// Split partials travel between workgroups (possibly on different XCDs, whose L2s are not
+// coherent) as relaxed agent-scope atomics: the stores write through (sc1) and the loads read
+// coherently, so no L2 writeback fence is needed; the writer waits for its stores
+// (vmcnt(0)) before taking the ticket.
+__device__ inline void st_coherent(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ inline float ld_coherent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline void st_coherent2(float* p, float a, float b) {
+  union { float f[2]; uint64_t u; } x;
+  x.f[0] = a;
+  x.f[1] = b;
+  __hip_atomic_store((uint64_t*)p, x.u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline float2 ld_coherent2(const float* p) {
+  union { float f[2]; uint64_t u; } x;
+  x.u = __hip_atomic_load((uint64_t*)const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return make_float2(x.f[0], x.f[1]);
+}
+__device__ inline void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 }  // namespace bg

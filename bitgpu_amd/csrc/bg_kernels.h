@@ -59,6 +59,10 @@ struct AttnArgs {
   int num_cus;
 };
 hipError_t launch_attention_f32(const LayerView& L, const AttnArgs& a, hipStream_t st);
+// split-K f32 decode / verify (G*S <= 16 rows per kv head), workspace as for the decode kernel
+hipError_t launch_attention_f32_split(const LayerView& L, const AttnArgs& a, hipStream_t st);
+bool f32_split_supported(const LayerView& L, int S, int H);
+size_t f32_workspace_floats(const LayerView& L, int S, int H);
 hipError_t launch_attention_decode(const LayerView& L, const AttnArgs& a, hipStream_t st);
 hipError_t launch_attention_prefill(const LayerView& L, const AttnArgs& a, hipStream_t st);
 // workspace floats needed by the decode kernel for S rows of H heads
