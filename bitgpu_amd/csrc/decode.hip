@@ -539,27 +539,47 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
   const __amdgpu_buffer_rsrc_t mrs = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(p.ws_ml + (size_t)kvh * NS * R * 2), (short)0, 0x7fffffff, 0x00020000);
   constexpr int kSC1 = 16;                     // cache policy: sc1
-  constexpr int MAXL = 8;                      // partial float4 loads in flight per thread
+  // partial float4 loads in flight per thread (D=256 partials are twice as long and its four
+  // waves have a full SIMD's registers after the tile loop)
+  constexpr int MAXL = D == 128 ? 8 : 16;
   const int C4 = R * D / 4;
   const int TPC = NTHR >= C4 ? NTHR / C4 : 1;  // threads per float4 column
   const int CPT = NTHR / TPC;                  // columns per pass
   float* wts = (float*)smem;                   // [NS][R] merge weights
   float* mls = wts + NS * R;                   // [NS][R][2]
   float4* red = (float4*)(mls + 2 * NS * R);   // [TPC][CPT] partial sums
-  // (1) (m, l) of every split -> LDS, while the first batch of partials is already in flight
+  // (1) (m, l) of every split -> LDS, while the first batch of partials is already in flight;
+  // the (m, l) loads go first (loads complete in order, so waiting for them does not wait for
+  // the batch behind them)
+  constexpr int MLMAX = 4;
+  uint2 mlv[MLMAX];
+#pragma unroll
+  for (int j = 0; j < MLMAX; j++) {
+    const int i = min(tid + j * NTHR, NS * R - 1);
+    mlv[j] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(mrs, i * 8, 0, kSC1));
+  }
   floatx4 pre[MAXL];
   {
     const int c = tid % CPT, k = tid / CPT;
     const bool act = c < C4 && k < TPC;
+    // branch-free (an out-of-range split re-reads the last one and gets weight 0), so all loads
+    // of a batch stay in flight together
 #pragma unroll
     for (int i = 0; i < MAXL; i++) {
-      const int sp = k + TPC * i;
-      pre[i] = (act && sp < NS) ? __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(
-                                      wrs, (sp * R * D + 4 * c) * 4, 0, kSC1))
-                                : floatx4{0, 0, 0, 0};
+      const int sp = min(k + TPC * i, NS - 1);
+      const int cc = act ? c : 0;
+      pre[i] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(wrs, (sp * R * D + 4 * cc) * 4, 0, kSC1));
     }
   }
-  for (int i = tid; i < NS * R; i += NTHR) {
+  // unconditional: an out-of-range slot rewrites the last element with its own value (a
+  // conditional store would pull its load into the branch and wait for the whole batch)
+#pragma unroll
+  for (int j = 0; j < MLMAX; j++) {
+    const int i = min(tid + j * NTHR, NS * R - 1);
+    mls[2 * i] = __uint_as_float(mlv[j].x);
+    mls[2 * i + 1] = __uint_as_float(mlv[j].y);
+  }
+  for (int i = tid + MLMAX * NTHR; i < NS * R; i += NTHR) {  // very long contexts only
     const uint2 u = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(mrs, i * 8, 0, kSC1));
     mls[2 * i] = __uint_as_float(u.x);
     mls[2 * i + 1] = __uint_as_float(u.y);
@@ -577,7 +597,9 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     for (int sp = lane; sp < NS; sp += 64) wts[sp * R + rho] = exp2f(mls[2 * (sp * R + rho)] - mx) * inv;
   }
   __syncthreads();
-  // (3) weighted sum of the partials, TPC threads per column, MAXL loads in flight per thread
+  // (3) weighted sum of the partials, TPC threads per column, MAXL loads in flight per thread;
+  // the next batch is issued before the current one is consumed (loads past the last split
+  // re-read it and get weight 0)
   for (int c0 = 0; c0 < C4; c0 += CPT) {
     const int c = c0 + tid % CPT;
     const int k = tid / CPT;
@@ -585,20 +607,15 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     if (act) {
       const int rho = (4 * c) / D;
-      for (int b0 = 0; b0 < NS; b0 += TPC * MAXL) {
-        floatx4 v[MAXL];
-        if (b0 == 0 && c0 == 0) {
+      const int BS = TPC * MAXL;  // splits per batch
+      auto issue = [&](floatx4 (&v)[MAXL], int b0) {
 #pragma unroll
-          for (int i = 0; i < MAXL; i++) v[i] = pre[i];
-        } else {
-#pragma unroll
-          for (int i = 0; i < MAXL; i++) {
-            const int sp = b0 + k + TPC * i;
-            v[i] = sp < NS ? __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(
-                                 wrs, (sp * R * D + 4 * c) * 4, 0, kSC1))
-                           : floatx4{0, 0, 0, 0};
-          }
+        for (int i = 0; i < MAXL; i++) {
+          const int sp = min(b0 + k + TPC * i, NS - 1);
+          v[i] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(wrs, (sp * R * D + 4 * c) * 4, 0, kSC1));
         }
+      };
+      auto consume = [&](const floatx4 (&v)[MAXL], int b0) {
 #pragma unroll
         for (int i = 0; i < MAXL; i++) {
           const int sp = b0 + k + TPC * i;
@@ -608,6 +625,20 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
           acc.z += v[i][2] * w;
           acc.w += v[i][3] * w;
         }
+      };
+      floatx4 va[MAXL], vb[MAXL];
+      if (c0 == 0) {
+#pragma unroll
+        for (int i = 0; i < MAXL; i++) va[i] = pre[i];
+      } else {
+        issue(va, 0);
+      }
+      for (int b0 = 0; b0 < NS; b0 += 2 * BS) {
+        issue(vb, b0 + BS);
+        consume(va, b0);
+        if (b0 + BS >= NS) break;
+        issue(va, b0 + 2 * BS);
+        consume(vb, b0 + BS);
       }
       red[(size_t)k * CPT + (c - c0)] = acc;
     }
