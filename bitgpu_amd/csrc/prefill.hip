@@ -349,9 +349,29 @@ __global__ __launch_bounds__(256 * TEAMS) void prefill_kernel(PrefillParams p) {
     // the earliest key index any row of the block masks (causal diagonal or scan end)
     const int mask_from = min(min(p.pos_base + s0 + 1, n_scan), p.phys_limit);
 
-    // ---------------- prologue: Q gather and the first tile, loads issued together ----------------
-    float4 qraw[2 * NC];
-    {
+    // ---------------- prologue: Q and the first tile, loads issued together ----------------
+    // Two teams (D=128): the block's 128 Q rows (f32, 64 KB) are read once per workgroup, as
+    // row-contiguous 32-byte pieces over all 512 threads, converted to the pre-scaled f16
+    // operand layout and put in the idle second buffer set; each wave then reads its Q^T
+    // operand from there. One team (D=256): each lane gathers its own operand.
+    constexpr bool QLDS = TEAMS == 2;
+    float4 qraw[QLDS ? 8 : 2 * NC];
+    int qunit[QLDS ? 4 : 1];
+    if constexpr (QLDS) {
+      int ln = tid, Gq = G;
+      asm volatile("" : "+v"(ln), "+s"(Gq));  // this lane math stays in the prologue
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int u = i * 512 + ln;   // 8-dim unit: row u / 16, dims 8 * (u % 16) ..
+        const int rr = u >> 4;
+        const int qq = s0 + rr / Gq, hh = kvh * Gq + rr % Gq;
+        const bool ok = rr < p.QB * Gq && qq < p.S;
+        const float* src = p.q + ((size_t)(ok ? qq : 0) * p.H + (ok ? hh : 0)) * D + 8 * (u & 15);
+        qraw[2 * i] = *(const float4*)src;
+        qraw[2 * i + 1] = *(const float4*)(src + 4);
+        qunit[i] = ok ? u : -1 - u;
+      }
+    } else {
       const float* qr = p.q + ((size_t)(row_ok ? qi : 0) * p.H + (row_ok ? h : 0)) * D;
 #pragma unroll
       for (int c = 0; c < NC; c++) {
@@ -370,14 +390,27 @@ __global__ __launch_bounds__(256 * TEAMS) void prefill_kernel(PrefillParams p) {
     }
     // Q^T operand: dims 16c + 8*g2 + [0..8), pre-scaled by scale*log2(e)
     half8p qf[NC];
-    {
+    auto to_h8 = [](const float4& a, const float4& b, float sc) {
+      return half8p{(_Float16)(a.x * sc), (_Float16)(a.y * sc), (_Float16)(a.z * sc), (_Float16)(a.w * sc),
+                    (_Float16)(b.x * sc), (_Float16)(b.y * sc), (_Float16)(b.z * sc), (_Float16)(b.w * sc)};
+    };
+    // operand area [row block][c][lane] of 16 bytes in the second buffer set (lk1, 32 KB)
+    _Float16* const qop = lk1;
+    if constexpr (QLDS) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const bool ok = qunit[i] >= 0;
+        const int u = ok ? qunit[i] : -1 - qunit[i];
+        const int rr = u >> 4, j = u & 15;
+        const int at = ((rr >> 5) * NC + (j >> 1)) * 64 + (rr & 31) + 32 * (j & 1);
+        PH8 hq;
+        hq.h = to_h8(qraw[2 * i], qraw[2 * i + 1], ok ? p.qscale : 0.0f);
+        stv(qop + (size_t)at * 8, hq.u);
+      }
+    } else {
       const float sc = row_ok ? p.qscale : 0.0f;
 #pragma unroll
-      for (int c = 0; c < NC; c++) {
-        const float4 a = qraw[2 * c], b = qraw[2 * c + 1];
-        qf[c] = half8p{(_Float16)(a.x * sc), (_Float16)(a.y * sc), (_Float16)(a.z * sc), (_Float16)(a.w * sc),
-                       (_Float16)(b.x * sc), (_Float16)(b.y * sc), (_Float16)(b.z * sc), (_Float16)(b.w * sc)};
-      }
+      for (int c = 0; c < NC; c++) qf[c] = to_h8(qraw[2 * c], qraw[2 * c + 1], sc);
     }
     if constexpr (!DMA) stg.store(R0, p, j00, k0, v0);
 
@@ -389,6 +422,15 @@ __global__ __launch_bounds__(256 * TEAMS) void prefill_kernel(PrefillParams p) {
     float m = -1e30f, lsum = 0.0f;
     if constexpr (DMA) __builtin_amdgcn_s_waitcnt(0xf70);  // vmcnt(0): this wave's copies landed
     __syncthreads();
+    if constexpr (QLDS) {
+#pragma unroll
+      for (int c = 0; c < NC; c++) {
+        PH8 hq;
+        hq.u = ldv(qop + (size_t)((wt * NC + c) * 64 + lane) * 8);
+        qf[c] = hq.h;
+      }
+      __syncthreads();  // every wave has its operand before step 0 stages into this buffer set
+    }
 
     // ---------------- one step: stage step s+1 into (kn, vn), compute step s from (kc, vc) ----------------
     auto step = [&](int s, const _Float16* kc, const _Float16* vc, _Float16* kn, _Float16* vn) {
