@@ -202,7 +202,7 @@ __global__ __launch_bounds__(256) void attn_f32_split_kernel(LayerView L, AttnAr
       const float* st = L.sin_tab + (size_t)ri * (D / 2) + i0;
 #pragma unroll
       for (int i = 0; i < DQ; i++) {
-        const float other = __shfl_xor(k[i], 32, 64);
+        const float other = xor32(k[i]);
         const float rv = g < 2 ? -other : other;
         k[i] = __fadd_rn(__fmul_rn(k[i], ct[i]), __fmul_rn(rv, st[i]));
       }
@@ -214,8 +214,8 @@ __global__ __launch_bounds__(256) void attn_f32_split_kernel(LayerView L, AttnAr
       float dot = 0.0f;
 #pragma unroll
       for (int i = 0; i < DQ; i++) dot = fmaf(qr[i], k[i], dot);
-      dot += __shfl_xor(dot, 16, 64);
-      dot += __shfl_xor(dot, 32, 64);
+      { const float2 r = pair16(dot); dot = r.x + r.y; }
+      { const float2 r = pair32(dot); dot = r.x + r.y; }
       const int s = r / sp.G;
       const bool ok = r < R && P < sp.n_scan && P < sp.phys_limit && Lg <= a.pos_base + s;
       x[r] = ok ? dot : -INFINITY;

@@ -74,28 +74,64 @@ __device__ inline int q8_code(float v, float s) {
 }
 __device__ inline float q8_scale_of(float absmax) { return fmaxf(absmax, 1e-30f); }
 
-// ---- wave64 reductions (DPP/permute via the compiler's cross-lane builtins) ----
-__device__ inline float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+// ---- cross-lane exchange and reductions, all in the VALU (no LDS round trip) ----
+// Inside a 16-lane row: DPP quad_perm [1,0,3,2] and [2,3,0,1] pair lanes i^1 and i^2; once a
+// quad holds one value, row_half_mirror (lane 7-i of each 8) and then row_mirror (lane 15-i)
+// pair it with the other quad and the other half. Across rows: v_permlane16_swap swaps the odd
+// rows of its first operand with the even rows of its second, v_permlane32_swap the upper half
+// of the first with the lower half of the second; swapping a value with itself leaves the two
+// results holding x[l] and x[l ^ 16] (or x[l ^ 32]) in some order.
+template <int CTRL>
+__device__ inline float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;
+constexpr int kDppMirror = 0x140;
+// {x[l], x[l^16]} and {x[l], x[l^32]} as an unordered pair
+__device__ inline float2 pair16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ inline float2 pair32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+// x[l ^ 32] (the other half of the wave)
+__device__ inline float xor32(float v) {
+  const float2 r = pair32(v);
+  return (__lane_id() < 32) ? r.y : r.x;
+}
+// reduce over aligned groups of N lanes (N = 2, 4, 8, 16, 32, 64); every lane of a group gets
+// the same bits
+template <int N>
+__device__ inline float group_max(float v) {
+  static_assert(N == 2 || N == 4 || N == 8 || N == 16 || N == 32 || N == 64, "group size");
+  v = fmaxf(v, dpp_mov<kDppXor1>(v));
+  if constexpr (N >= 4) v = fmaxf(v, dpp_mov<kDppXor2>(v));
+  if constexpr (N >= 8) v = fmaxf(v, dpp_mov<kDppHalfMirror>(v));
+  if constexpr (N >= 16) v = fmaxf(v, dpp_mov<kDppMirror>(v));
+  if constexpr (N >= 32) { const float2 r = pair16(v); v = fmaxf(r.x, r.y); }
+  if constexpr (N >= 64) { const float2 r = pair32(v); v = fmaxf(r.x, r.y); }
   return v;
 }
-__device__ inline float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+template <int N>
+__device__ inline float group_sum(float v) {
+  static_assert(N == 2 || N == 4 || N == 8 || N == 16 || N == 32 || N == 64, "group size");
+  v += dpp_mov<kDppXor1>(v);
+  if constexpr (N >= 4) v += dpp_mov<kDppXor2>(v);
+  if constexpr (N >= 8) v += dpp_mov<kDppHalfMirror>(v);
+  if constexpr (N >= 16) v += dpp_mov<kDppMirror>(v);
+  if constexpr (N >= 32) { const float2 r = pair16(v); v = r.x + r.y; }
+  if constexpr (N >= 64) { const float2 r = pair32(v); v = r.x + r.y; }
   return v;
 }
+__device__ inline float wave_sum(float v) { return group_sum<64>(v); }
+__device__ inline float wave_max(float v) { return group_max<64>(v); }
 // reduce over the 16 lanes of a lane group (lanes 16g .. 16g+15)
-__device__ inline float group16_max(float v) {
-#pragma unroll
-  for (int o = 8; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
-}
-__device__ inline float group16_sum(float v) {
-#pragma unroll
-  for (int o = 8; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
+__device__ inline float group16_max(float v) { return group_max<16>(v); }
+__device__ inline float group16_sum(float v) { return group_sum<16>(v); }
 
 // Split partials travel between workgroups (possibly on different XCDs, whose L2s are not
 // coherent) as relaxed agent-scope atomics: the stores write through (sc1) and the loads read

@@ -16,8 +16,7 @@ __device__ inline void store_row(const LayerView& L, int which, int slot, int kv
     float m = 0.0f;
 #pragma unroll
     for (int e = 0; e < EPL; e++) m = fmaxf(m, fabsf(v[e]));
-#pragma unroll
-    for (int o = LPB / 2; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    m = group_max<LPB>(m);
     const float s = q8_scale_of(m);
     float* sc = which == 0 ? L.ks : L.vs;
     if ((lane % LPB) == 0) sc[scale_offset(kvh, slot, d0 / kBlock, L.cap, D)] = s;

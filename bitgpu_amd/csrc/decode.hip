@@ -372,15 +372,15 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
             v[e] = c[0][e];
           }
         }
-        // reduce-scatter over the 4 lane groups: lane group g ends with query row g of the pass
-        const bool lowg = g < 2;
-        const float s0 = __shfl_xor(lowg ? v[2] : v[0], 32, 64);
-        const float s1 = __shfl_xor(lowg ? v[3] : v[1], 32, 64);
-        const float k0 = (lowg ? v[0] : v[2]) + s0;
-        const float k1 = (lowg ? v[1] : v[3]) + s1;
-        const bool odd = g & 1;
-        const float s2 = __shfl_xor(odd ? k0 : k1, 16, 64);
-        sc[t2] = (odd ? k1 : k0) + s2;
+        // reduce-scatter over the 4 lane groups: lane group g ends with query row g of the pass.
+        // permlane32_swap(a, b) leaves lanes l < 32 with {a[l], a[l+32]} and lanes l >= 32 with
+        // {b[l-32], b[l]}; permlane16_swap does the same for odd/even row pairs.
+        const auto u0 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[0]), __float_as_uint(v[2]), false, false);
+        const auto u1 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[1]), __float_as_uint(v[3]), false, false);
+        const float k0 = __uint_as_float(u0[0]) + __uint_as_float(u0[1]);  // rows 0,1: dims of v[0]; rows 2,3: v[2]
+        const float k1 = __uint_as_float(u1[0]) + __uint_as_float(u1[1]);
+        const auto u2 = __builtin_amdgcn_permlane16_swap(__float_as_uint(k0), __float_as_uint(k1), false, false);
+        sc[t2] = __uint_as_float(u2[0]) + __uint_as_float(u2[1]);
       }
       // mask + online softmax for row rho = 4*pass + g
       const int rho = 4 * pass + g;

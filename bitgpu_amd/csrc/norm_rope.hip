@@ -44,8 +44,7 @@ __device__ inline void store_vgroup(const LayerView& L, int kvh, int slot_base, 
       float m = 0.0f;
 #pragma unroll
       for (int e = 0; e < EPL; e++) m = fmaxf(m, fabsf(v[j][e]));
-#pragma unroll
-      for (int o = LPB / 2; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+      m = group_max<LPB>(m);
       sc[j] = q8_scale_of(m);
       if ((lane % LPB) == 0) L.vs[scale_offset(kvh, slot_base + j, d0 / kBlock, L.cap, D)] = sc[j];
     }

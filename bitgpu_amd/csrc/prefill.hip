@@ -489,7 +489,7 @@ __global__ __launch_bounds__(256 * TEAMS) void prefill_kernel(PrefillParams p) {
             mt = fmaxf(mt, x[u][e]);
           }
       }
-      mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+      { const float2 r = pair32(mt); mt = fmaxf(r.x, r.y); }
       // raise the reference max only when this step's max exceeds it by more than 2^8
       const bool grow = mt > m + 8.0f;
       if (__any(grow)) {
@@ -564,7 +564,7 @@ __global__ __launch_bounds__(256 * TEAMS) void prefill_kernel(PrefillParams p) {
     }
     // ---------------- store ----------------
     if (team == 0) {
-      lsum += __shfl_xor(lsum, 32, 64);
+      { const float2 r = pair32(lsum); lsum = r.x + r.y; }
       if constexpr (TEAMS == 2) {
         // through this wave's own merge region: rows written swizzled, read back and stored as
         // contiguous 512-byte rows (the register layout scatters 16 bytes per row)
