@@ -9,8 +9,8 @@
 //           GQA group are served by one read of each K/V byte.
 //   QK    = v_mfma_f32_16x16x32_f16 with K as the B operand (lane = slot, 8 dims per lane
 //           group) and a block-diagonal Q as A: row group g of the 16 output rows only sees the
-//           dims lane group g loaded, so the MFMA returns 4 partial dot products per slot that a
-//           3-shuffle reduce-scatter turns into one full score per lane -- no 12/16 padding rows.
+//           dims lane group g loaded, so the MFMA returns 4 partial dot products per slot that
+//           three permlane swaps reduce-scatter into one full score per lane -- no padding rows.
 //           q8 codes enter the MFMA as exact f16 integers (xor/perm/pk_add, no float convert);
 //           the per-32 block scale multiplies the MFMA result. Q is split hi+lo f16 so the
 //           product keeps ~f32 accuracy.
@@ -30,6 +30,7 @@ namespace bg {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4v __attribute__((ext_vector_type(4)));
 
 constexpr int NW = 4;  // waves per workgroup
 constexpr float kLog2e = 1.4426950408889634f;
@@ -101,7 +102,8 @@ struct DecodeSmem {
   __host__ __device__ static size_t q_bytes(int np) { return (size_t)np * NT * 2 * 64 * 16 + 32; }
   static constexpr size_t p_bytes_wave = (size_t)NBV * RS * 32 * 2;
   static constexpr size_t c_bytes_wave = (size_t)RS * 4;
-  __host__ __device__ static size_t merge_bytes(int R) { return (size_t)NW * R * (D + 2) * 4; }
+  static constexpr int DP = D + 4;                        // padded row of a wave partial
+  __host__ __device__ static size_t merge_bytes(int R) { return (size_t)NW * R * (DP + 1) * 4; }
   __host__ __device__ static size_t total(int np, int R) {
     size_t a = q_bytes(np) + NW * (p_bytes_wave + c_bytes_wave);
     size_t b = merge_bytes(R);
@@ -462,60 +464,83 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
   }
 
   // ---------------- combine the waves of the workgroup ----------------
+  // The row maxima go through an LDS array of their own (the tile loop never touches it), so
+  // one barrier publishes them and ends every wave's use of the tile-loop space. Each wave then
+  // rescales its own o and l to the workgroup maximum of the row and stores them as float4
+  // (rows padded by 4 floats to spread the banks); the sum over the waves is plain adds.
+  __shared__ float s_mw[NW][RS];
+#pragma unroll
+  for (int pass = 0; pass < SM::NPMAX; pass++) {
+    if (pass >= NP) break;
+    const int rho = 4 * pass + g;
+    if (n == 0 && rho < p.R) s_mw[wave][rho] = m[pass];
+  }
   __syncthreads();
-  float* mw = (float*)smem;               // [NW][R]
-  float* lw = mw + NW * p.R;              // [NW][R]
-  float* ow = lw + NW * p.R;              // [NW][R][D]
+  constexpr int DP = SM::DP;
+  float* lw = (float*)smem;               // [NW][R]
+  float* ow = lw + NW * p.R;              // [NW][R][DP]
+  auto row_max = [&](int rho) {
+    float M = s_mw[0][rho];
+#pragma unroll
+    for (int w = 1; w < NW; w++) M = fmaxf(M, s_mw[w][rho]);
+    return M;
+  };
 #pragma unroll
   for (int pass = 0; pass < SM::NPMAX; pass++) {
     if (pass >= NP) break;
     const float lt = group16_sum(lsum[pass]);
     const int rho = 4 * pass + g;
-    if (n == 0 && rho < p.R) {
-      mw[wave * p.R + rho] = m[pass];
-      lw[wave * p.R + rho] = lt;
-    }
+    if (n == 0 && rho < p.R) lw[wave * p.R + rho] = lt * __builtin_amdgcn_exp2f(m[pass] - row_max(rho));
   }
 #pragma unroll
   for (int st = 0; st < NSET; st++) {
     const int rho = 16 * st + n;
     if (rho < p.R) {
+      const float f = __builtin_amdgcn_exp2f(s_mw[wave][rho] - row_max(rho));
+      float* orow = ow + ((size_t)wave * p.R + rho) * DP + 8 * g;
+      // o[st][2b + par][e] holds dim 32b + 8g + 2e + par: dims 32b + 8g + 4h .. +3 are
+      // (e, par) = (2h, 0), (2h, 1), (2h + 1, 0), (2h + 1, 1)
 #pragma unroll
       for (int b = 0; b < NB; b++)
 #pragma unroll
-        for (int par = 0; par < 2; par++)
-#pragma unroll
-          for (int e = 0; e < 4; e++) {
-            const int d = 32 * b + 2 * (4 * g + e) + par;
-            ow[((size_t)wave * p.R + rho) * D + d] = o[st][2 * b + par][e];
-          }
+        for (int h = 0; h < 2; h++)
+          *(float4*)(orow + 32 * b + 4 * h) = make_float4(o[st][2 * b][2 * h] * f, o[st][2 * b + 1][2 * h] * f,
+                                                          o[st][2 * b][2 * h + 1] * f, o[st][2 * b + 1][2 * h + 1] * f);
     }
   }
   __syncthreads();
 
   const bool single = p.n_splits == 1;
-  float* wso = p.ws_o + ((size_t)kvh * p.n_splits + split) * p.R * D;
+  constexpr int kSC1 = 16;  // cache policy sc1: agent-coherent (written through / read from memory)
+  const int C4 = p.R * (D / 4);
   float* wsml = p.ws_ml + ((size_t)kvh * p.n_splits + split) * p.R * 2;
-  for (int idx = tid; idx < p.R * D; idx += NTHR) {
-    const int rho = idx / D, d = idx % D;
-    float M = -1e30f;
-#pragma unroll
-    for (int w = 0; w < NW; w++) M = fmaxf(M, mw[w * p.R + rho]);
-    float acc = 0.0f, lt = 0.0f;
+  const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(single ? p.out : p.ws_o + ((size_t)kvh * p.n_splits + split) * p.R * D), (short)0, 0x7fffffff, 0x00020000);
+  for (int c = tid; c < C4; c += NTHR) {
+    const int rho = c / (D / 4), d = 4 * (c % (D / 4));
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    float lt = 0.0f;
 #pragma unroll
     for (int w = 0; w < NW; w++) {
-      const float f = exp2f(mw[w * p.R + rho] - M);
-      acc += ow[((size_t)w * p.R + rho) * D + d] * f;
-      lt += lw[w * p.R + rho] * f;
+      const float4 v = *(const float4*)(ow + ((size_t)w * p.R + rho) * DP + d);
+      acc.x += v.x;
+      acc.y += v.y;
+      acc.z += v.z;
+      acc.w += v.w;
+      lt += lw[w * p.R + rho];
     }
     if (single) {
       const int s = rho / p.G, h = kvh * p.G + rho % p.G;
-      float r = acc / lt;
-      if (p.gate) r = r / (1.0f + expf(-p.gate[((size_t)s * p.H + h) * p.gate_stride + d]));
-      p.out[((size_t)s * p.H + h) * D + d] = r;
+      float r[4] = {acc.x / lt, acc.y / lt, acc.z / lt, acc.w / lt};
+      if (p.gate) {
+        const float* gr = p.gate + ((size_t)s * p.H + h) * p.gate_stride + d;
+#pragma unroll
+        for (int e = 0; e < 4; e++) r[e] = r[e] / (1.0f + expf(-gr[e]));
+      }
+      *(float4*)(p.out + ((size_t)s * p.H + h) * D + d) = make_float4(r[0], r[1], r[2], r[3]);
     } else {
-      st_coherent(&wso[idx], acc);
-      if (d == 0) st_coherent2(&wsml[2 * rho], M, lt);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4v, acc), ors, (rho * D + d) * 4, 0, kSC1);
+      if (d == 0) st_coherent2(&wsml[2 * rho], row_max(rho), lt);
     }
   }
   if (single) return;
@@ -530,33 +555,33 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
   }
   __syncthreads();
   if (!s_last) return;
-  // Coherent reads of the other workgroups' partials: buffer loads with the sc1 (agent
-  // coherence) cache policy -- ordinary loads to the compiler, so a batch stays in flight.
+  // Coherent reads of the other workgroups' partials: buffer loads with the sc1 cache policy --
+  // ordinary loads to the compiler, so a batch stays in flight.
   const int NS = p.n_splits;
   const int R = p.R;
   const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(p.ws_o + (size_t)kvh * NS * R * D), (short)0, 0x7fffffff, 0x00020000);
   const __amdgpu_buffer_rsrc_t mrs = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(p.ws_ml + (size_t)kvh * NS * R * 2), (short)0, 0x7fffffff, 0x00020000);
-  constexpr int kSC1 = 16;                     // cache policy: sc1
   // partial float4 loads in flight per thread (D=256 partials are twice as long and its four
   // waves have a full SIMD's registers after the tile loop)
   constexpr int MAXL = D == 128 ? 8 : 16;
-  const int C4 = R * D / 4;
   const int TPC = NTHR >= C4 ? NTHR / C4 : 1;  // threads per float4 column
   const int CPT = NTHR / TPC;                  // columns per pass
   float* wts = (float*)smem;                   // [NS][R] merge weights
-  float* mls = wts + NS * R;                   // [NS][R][2]
+  float* mls = wts + NS * R;                   // [NS][R][2] (split lists longer than a wave)
   float4* red = (float4*)(mls + 2 * NS * R);   // [TPC][CPT] partial sums
-  // (1) (m, l) of every split -> LDS, while the first batch of partials is already in flight;
-  // the (m, l) loads go first (loads complete in order, so waiting for them does not wait for
-  // the batch behind them)
-  constexpr int MLMAX = 4;
-  uint2 mlv[MLMAX];
+  // (1) (m, l) of the splits. Up to 64 splits: a wave takes a row, one split per lane, in
+  // registers. Issued first and unconditionally (indices clamped), so waiting for them does not
+  // wait for the partials behind them.
+  constexpr int RPW = (RS + NW - 1) / NW;      // rows per wave
+  const bool lane_split = NS <= 64;
+  uint2 mlv[RPW];
 #pragma unroll
-  for (int j = 0; j < MLMAX; j++) {
-    const int i = min(tid + j * NTHR, NS * R - 1);
-    mlv[j] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(mrs, i * 8, 0, kSC1));
+  for (int k = 0; k < RPW; k++) {
+    const int rho = min(wave + k * NW, R - 1);
+    const int sp = min(lane, NS - 1);
+    mlv[k] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(mrs, (sp * R + rho) * 8, 0, kSC1));
   }
   floatx4 pre[MAXL];
   {
@@ -571,35 +596,43 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
       pre[i] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(wrs, (sp * R * D + 4 * cc) * 4, 0, kSC1));
     }
   }
-  // unconditional: an out-of-range slot rewrites the last element with its own value (a
-  // conditional store would pull its load into the branch and wait for the whole batch)
+  // (2) weights w[sp][rho] = 2^(m_sp - M) / sum_sp l_sp 2^(m_sp - M)
+  if (lane_split) {
 #pragma unroll
-  for (int j = 0; j < MLMAX; j++) {
-    const int i = min(tid + j * NTHR, NS * R - 1);
-    mls[2 * i] = __uint_as_float(mlv[j].x);
-    mls[2 * i + 1] = __uint_as_float(mlv[j].y);
-  }
-  for (int i = tid + MLMAX * NTHR; i < NS * R; i += NTHR) {  // very long contexts only
-    const uint2 u = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(mrs, i * 8, 0, kSC1));
-    mls[2 * i] = __uint_as_float(u.x);
-    mls[2 * i + 1] = __uint_as_float(u.y);
-  }
-  __syncthreads();
-  // (2) weights: one wave per row, lanes over splits
-  for (int rho = wave; rho < R; rho += NW) {
-    float mx = -1e30f;
-    for (int sp = lane; sp < NS; sp += 64) mx = fmaxf(mx, mls[2 * (sp * R + rho)]);
-    mx = wave_max(mx);
-    float lt = 0.0f;
-    for (int sp = lane; sp < NS; sp += 64) lt += mls[2 * (sp * R + rho) + 1] * exp2f(mls[2 * (sp * R + rho)] - mx);
-    lt = wave_sum(lt);
-    const float inv = 1.0f / lt;
-    for (int sp = lane; sp < NS; sp += 64) wts[sp * R + rho] = exp2f(mls[2 * (sp * R + rho)] - mx) * inv;
+    for (int k = 0; k < RPW; k++) {
+      const int rho = wave + k * NW;
+      if (rho < R) {
+        const bool ok = lane < NS;
+        const float mi = ok ? __uint_as_float(mlv[k].x) : -INFINITY;
+        const float li = ok ? __uint_as_float(mlv[k].y) : 0.0f;
+        const float M = wave_max(mi);
+        const float e = __builtin_amdgcn_exp2f(mi - M);
+        const float lt = wave_sum(li * e);
+        if (ok) wts[lane * R + rho] = e / lt;
+      }
+    }
+  } else {
+    for (int i = tid; i < NS * R; i += NTHR) {
+      const uint2 u = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(mrs, i * 8, 0, kSC1));
+      mls[2 * i] = __uint_as_float(u.x);
+      mls[2 * i + 1] = __uint_as_float(u.y);
+    }
+    __syncthreads();
+    for (int rho = wave; rho < R; rho += NW) {
+      float mx = -INFINITY;
+      for (int sp = lane; sp < NS; sp += 64) mx = fmaxf(mx, mls[2 * (sp * R + rho)]);
+      mx = wave_max(mx);
+      float lt = 0.0f;
+      for (int sp = lane; sp < NS; sp += 64) lt += mls[2 * (sp * R + rho) + 1] * __builtin_amdgcn_exp2f(mls[2 * (sp * R + rho)] - mx);
+      lt = wave_sum(lt);
+      for (int sp = lane; sp < NS; sp += 64) wts[sp * R + rho] = __builtin_amdgcn_exp2f(mls[2 * (sp * R + rho)] - mx) / lt;
+    }
   }
   __syncthreads();
   // (3) weighted sum of the partials, TPC threads per column, MAXL loads in flight per thread;
-  // the next batch is issued before the current one is consumed (loads past the last split
-  // re-read it and get weight 0)
+  // with more than one batch the next is issued before the current one is consumed (loads past
+  // the last split re-read it and get weight 0)
+  const int BS = TPC * MAXL;  // splits per batch
   for (int c0 = 0; c0 < C4; c0 += CPT) {
     const int c = c0 + tid % CPT;
     const int k = tid / CPT;
@@ -607,7 +640,6 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     if (act) {
       const int rho = (4 * c) / D;
-      const int BS = TPC * MAXL;  // splits per batch
       auto issue = [&](floatx4 (&v)[MAXL], int b0) {
 #pragma unroll
         for (int i = 0; i < MAXL; i++) {
@@ -633,12 +665,16 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
       } else {
         issue(va, 0);
       }
-      for (int b0 = 0; b0 < NS; b0 += 2 * BS) {
-        issue(vb, b0 + BS);
-        consume(va, b0);
-        if (b0 + BS >= NS) break;
-        issue(va, b0 + 2 * BS);
-        consume(vb, b0 + BS);
+      if (NS <= BS) {
+        consume(va, 0);
+      } else {
+        for (int b0 = 0; b0 < NS; b0 += 2 * BS) {
+          issue(vb, b0 + BS);
+          consume(va, b0);
+          if (b0 + BS >= NS) break;
+          issue(va, b0 + 2 * BS);
+          consume(vb, b0 + BS);
+        }
       }
       red[(size_t)k * CPT + (c - c0)] = acc;
     }
@@ -740,7 +776,7 @@ static hipError_t launch_cfg(const LayerView& L, const AttnArgs& a, hipStream_t 
   const size_t cpt = (size_t)64 * NW / tpc;
   const size_t merge = (size_t)3 * sp.n_splits * p.R * 4 + tpc * cpt * 16;
   smem = smem > merge ? smem : merge;
-  if (smem > 160 * 1024) return hipErrorInvalidValue;
+  if (smem > 159 * 1024) return hipErrorInvalidValue;  // + static: wave maxima, ticket flag
   if (smem > 64 * 1024) {
     static size_t attr_bytes = 0;
     if (smem > attr_bytes) {
