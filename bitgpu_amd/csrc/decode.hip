@@ -87,6 +87,7 @@ struct DecodeParams {
   float* ws_o;       // [KV][n_splits][R][D]
   float* ws_ml;      // [KV][n_splits][R][2]
   unsigned* ws_count;  // [KV]
+  int merge_ext;     // 1: the splits only publish; decode_merge_kernel merges after this launch
 };
 
 // Shared memory plan (bytes): Q operands, per-wave P^T tiles, per-wave corr; after the tile
@@ -513,9 +514,9 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
   const bool single = p.n_splits == 1;
   constexpr int kSC1 = 16;  // cache policy sc1: agent-coherent (written through / read from memory)
   const int C4 = p.R * (D / 4);
-  float* wsml = p.ws_ml + ((size_t)kvh * p.n_splits + split) * p.R * 2;
-  const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(single ? p.out : p.ws_o + ((size_t)kvh * p.n_splits + split) * p.R * D), (short)0, 0x7fffffff, 0x00020000);
+  float* wso = single ? p.out : p.ws_o + ((size_t)kvh * p.n_splits + split) * p.R * D;
+  float* wsml = single ? p.out : p.ws_ml + ((size_t)kvh * p.n_splits + split) * p.R * 2;
+  const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc((void*)wso, (short)0, 0x7fffffff, 0x00020000);
   for (int c = tid; c < C4; c += NTHR) {
     const int rho = c / (D / 4), d = 4 * (c % (D / 4));
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -538,12 +539,15 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
         for (int e = 0; e < 4; e++) r[e] = r[e] / (1.0f + expf(-gr[e]));
       }
       *(float4*)(p.out + ((size_t)s * p.H + h) * D + d) = make_float4(r[0], r[1], r[2], r[3]);
+    } else if (p.merge_ext) {  // read by the next launch: plain stores
+      *(float4*)(wso + rho * D + d) = acc;
+      if (d == 0) *(float2*)&wsml[2 * rho] = make_float2(row_max(rho), lt);
     } else {
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4v, acc), ors, (rho * D + d) * 4, 0, kSC1);
       if (d == 0) st_coherent2(&wsml[2 * rho], row_max(rho), lt);
     }
   }
-  if (single) return;
+  if (single || p.merge_ext) return;
 
   // ---------------- last workgroup of this kv head merges the splits ----------------
   __shared__ unsigned s_last;
@@ -703,6 +707,56 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
 }
 
 // ------------------------------------------------------------------------------------------
+// Split merge as a launch of its own, for split lists whose partials are too many for one
+// workgroup to read quickly (n_splits * R * D * 4 bytes per kv head): one wave per (64-dim
+// chunk, row, kv head). Per chunk of up to 64 splits, lane s holds split s's (m, l) and every
+// lane loads its dim of all the chunk's partials at once; the chunk folds into a running
+// log-sum-exp (M, L, acc).
+struct MergeParams {
+  const float* ws_o;   // [KV][n_splits][R][D]
+  const float* ws_ml;  // [KV][n_splits][R][2]
+  int n_splits, R, G, H;
+  const float* gate;
+  int gate_stride;
+  float* out;
+};
+
+template <int D>
+__global__ __launch_bounds__(64) void decode_merge_kernel(MergeParams p) {
+  const int lane = threadIdx.x;
+  const int d = blockIdx.x * 64 + lane, rho = blockIdx.y, kvh = blockIdx.z;
+  const int NS = p.n_splits, R = p.R;
+  const float* o = p.ws_o + (size_t)kvh * NS * R * D + (size_t)rho * D + d;  // + sp * R * D
+  const float* ml = p.ws_ml + (size_t)kvh * NS * R * 2 + (size_t)rho * 2;    // + sp * R * 2
+  float M = -INFINITY, L = 0.0f, acc = 0.0f;
+  for (int s0 = 0; s0 < NS; s0 += 64) {
+    const int nc = min(64, NS - s0);
+    // unconditional loads (indices past the chunk re-read its last split, weight 0)
+    const float2 v = *(const float2*)(ml + (size_t)(s0 + min(lane, nc - 1)) * R * 2);
+    float ov[64];
+#pragma unroll
+    for (int j = 0; j < 64; j++) ov[j] = o[(size_t)(s0 + min(j, nc - 1)) * R * D];
+    const bool ok = lane < nc;
+    const float mi = ok ? v.x : -INFINITY;
+    const float Mn = fmaxf(M, wave_max(mi));
+    const float e = ok ? __builtin_amdgcn_exp2f(mi - Mn) : 0.0f;
+    const float sc = __builtin_amdgcn_exp2f(M - Mn);  // 0 on the first chunk
+    L = L * sc + wave_sum(ok ? v.y * e : 0.0f);
+    acc *= sc;
+#pragma unroll
+    for (int j = 0; j < 64; j++) acc = fmaf(ov[j], __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j)), acc);
+    M = Mn;
+  }
+  const int s = rho / p.G, h = kvh * p.G + rho % p.G;
+  float r = acc / L;
+  if (p.gate) r = r / (1.0f + expf(-p.gate[((size_t)s * p.H + h) * p.gate_stride + d]));
+  p.out[((size_t)s * p.H + h) * D + d] = r;
+}
+
+// partials per kv head above which the merge runs as its own launch (one workgroup reads
+// them at roughly 40-70 GB/s; the extra launch costs about 2 us)
+constexpr size_t kExtMergeBytes = 96 * 1024;
+
 static int nset_for(int R) { return (R + 15) / 16; }
 
 bool decode_supported(const LayerView& L, int S, int H) {
@@ -768,6 +822,7 @@ static hipError_t launch_cfg(const LayerView& L, const AttnArgs& a, hipStream_t 
   p.ws_o = a.ws_o;
   p.ws_ml = a.ws_o ? a.ws_o + (size_t)L.kv_heads * sp.n_splits * p.R * D : nullptr;
   p.ws_count = a.ws_count;
+  p.merge_ext = sp.n_splits > 1 && (size_t)sp.n_splits * p.R * D * 4 > kExtMergeBytes;
   const int NP = (p.R + 3) / 4;
   size_t smem = SM::total(NP, p.R);
   // the split merge reuses the space: weights + l [NS][R] and float4 partial sums
@@ -787,6 +842,19 @@ static hipError_t launch_cfg(const LayerView& L, const AttnArgs& a, hipStream_t 
     }
   }
   hipLaunchKernelGGL((decode_kernel<D, DT, ROLL, NSET, NW>), dim3(sp.n_splits * L.kv_heads), dim3(64 * NW), smem, st, p);
+  if (p.merge_ext) {
+    MergeParams m;
+    m.ws_o = p.ws_o;
+    m.ws_ml = p.ws_ml;
+    m.n_splits = p.n_splits;
+    m.R = p.R;
+    m.G = p.G;
+    m.H = p.H;
+    m.gate = p.gate;
+    m.gate_stride = p.gate_stride;
+    m.out = p.out;
+    hipLaunchKernelGGL((decode_merge_kernel<D>), dim3(D / 64, p.R, L.kv_heads), dim3(64), 0, st, m);
+  }
   return hipGetLastError();
 }
 

@@ -130,6 +130,19 @@ def test_decode_gate_hybrid_shape(dev):
     _check("q8", out, exp)
 
 
+# Split merges. On 256 CUs the split count is about 256 / KV; the merge runs inside the decode
+# launch (last workgroup of a kv head) up to 96 KB of partials per kv head, above that as a
+# launch of its own. Shapes: (24,4,256) L=4097 -> 33 splits x 6 rows x 1 KB (own launch);
+# (16,2,128) L=32768 -> 128 splits, two 64-split chunks (own launch); (2,2,128) L=32768 -> 128
+# splits of one row (in the launch, weights through LDS); (32,8,128) S=12 -> 48 rows (own launch).
+@pytest.mark.parametrize("dtype", ["f16", "q8"])
+@pytest.mark.parametrize("H,KV,D,L,S,gate", [(24, 4, 256, 4097, 1, True), (16, 2, 128, 32768, 1, False),
+                                             (2, 2, 128, 32768, 1, False), (32, 8, 128, 4108, 12, False)])
+def test_decode_merge_paths(dev, dtype, H, KV, D, L, S, gate):
+    out, exp = _raw_case(dtype, H, KV, D, L, S, seed=L + H, gate=gate)
+    _check(dtype, out, exp)
+
+
 # ------------------------------------------------------------------ f32 kernel
 @pytest.mark.parametrize("S,L", [(1, 1), (1, 100), (7, 40), (64, 64)])
 def test_f32_kernel(dev, S, L):
