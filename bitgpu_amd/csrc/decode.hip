@@ -759,12 +759,25 @@ constexpr size_t kExtMergeBytes = 96 * 1024;
 
 static int nset_for(int R) { return (R + 15) / 16; }
 
+// dynamic LDS of the tile loop and wave combine (DecodeSmem::total for the launch's template
+// arguments); the in-launch split merge needs less (at most 96 KB of partials per kv head)
+static size_t decode_lds_bytes(int D, int dtype, int R) {
+  const int nset = nset_for(R);
+  const int NW = (D == 128 && nset == 1) ? 8 : 4;
+  const int RS = 16 * nset, NT = D / 32, NBV = dtype == KV_Q8 ? D / 32 : 1;
+  const size_t a = (size_t)((R + 3) / 4) * NT * 2 * 64 * 16 + 32 + (size_t)NW * ((size_t)NBV * RS * 32 * 2 + (size_t)RS * 4);
+  const size_t b = (size_t)NW * R * (D + 5) * 4;
+  return a > b ? a : b;
+}
+constexpr size_t kDecodeLdsMax = 159 * 1024;  // + the static wave maxima and ticket flag
+
 bool decode_supported(const LayerView& L, int S, int H) {
   if (L.dtype == KV_F32) return false;
   if (L.D != 128 && L.D != 256) return false;
   const int G = H / L.kv_heads;
   const int R = G * S;
-  return R >= 1 && nset_for(R) <= 3;
+  // more rows than the operand and P^T tiles fit in LDS (D=256: about 20) go to the prefill kernel
+  return R >= 1 && nset_for(R) <= 3 && decode_lds_bytes(L.D, L.dtype, R) <= kDecodeLdsMax;
 }
 
 // waves per workgroup: 8 where the registers allow two workgroups' worth per CU, else 4
@@ -825,13 +838,16 @@ static hipError_t launch_cfg(const LayerView& L, const AttnArgs& a, hipStream_t 
   p.merge_ext = sp.n_splits > 1 && (size_t)sp.n_splits * p.R * D * 4 > kExtMergeBytes;
   const int NP = (p.R + 3) / 4;
   size_t smem = SM::total(NP, p.R);
-  // the split merge reuses the space: weights + l [NS][R] and float4 partial sums
-  const size_t C4 = (size_t)p.R * D / 4;
-  const size_t tpc = (size_t)64 * NW >= C4 ? (size_t)64 * NW / C4 : 1;
-  const size_t cpt = (size_t)64 * NW / tpc;
-  const size_t merge = (size_t)3 * sp.n_splits * p.R * 4 + tpc * cpt * 16;
-  smem = smem > merge ? smem : merge;
-  if (smem > 159 * 1024) return hipErrorInvalidValue;  // + static: wave maxima, ticket flag
+  if (smem != decode_lds_bytes(D, DT, p.R)) return hipErrorInvalidValue;  // the two plans agree
+  if (sp.n_splits > 1 && !p.merge_ext) {
+    // the in-launch merge reuses the space: weights + l [NS][R] and float4 partial sums
+    const size_t C4 = (size_t)p.R * D / 4;
+    const size_t tpc = (size_t)64 * NW >= C4 ? (size_t)64 * NW / C4 : 1;
+    const size_t cpt = (size_t)64 * NW / tpc;
+    const size_t merge = (size_t)3 * sp.n_splits * p.R * 4 + tpc * cpt * 16;
+    smem = smem > merge ? smem : merge;
+  }
+  if (smem > kDecodeLdsMax) return hipErrorInvalidValue;
   if (smem > 64 * 1024) {
     static size_t attr_bytes = 0;
     if (smem > attr_bytes) {
