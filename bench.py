@@ -183,6 +183,27 @@ def bench_prefill(torch, E, W, cfg, S, steps, warmup, seed):
             "tflops": round(fl / us_attn / 1e6, 1), "mfma_frac": round(fl / us_attn / 1e6 / MFMA_F16_PEAK_TFLOPS, 4)}
 
 
+def profile_prefill(torch, E, W, n):
+    """C2 (f16, S=2048) and C5 (q8, S=8192) prefill attention, n plain launches each, for
+    rocprofv3 --pmc counter passes (MFMA busy cycles, MFMA ops, LDS activity)."""
+    dev = "cuda"
+    for cfg, S in ((W.C2, W.C2_S), (W.C5, W.C5_PREFILL)):
+        q, k, v, g = W.prefill_inputs(cfg, S, 2)
+        c = E.KvCache(1, cfg.KV, cfg.D, cfg.kv, max_seq_len=S, capacity=S)
+        cos, sin = (torch.from_numpy(x).to(dev) for x in E.rope_tables(cfg.theta, cfg.rot, S))
+        ones = torch.ones(cfg.D, device=dev)
+        qt, kt, vt = (torch.from_numpy(x).to(dev) for x in (q, k, v))
+        gt = torch.from_numpy(g).to(dev) if g is not None else None
+        qr = torch.empty(S, cfg.H, cfg.D, device=dev)
+        out = torch.empty(S, cfg.H, cfg.D, device=dev)
+        E.qkv_prologue(c, 0, qt, kt, vt, S, cfg.H, ones, ones, cfg.eps, cos, sin, cfg.rot, 0, 0, q_out=qr)
+        for _ in range(n):
+            E.attention(c, 0, qr, S, cfg.H, 0, scale=float(1.0 / np.sqrt(cfg.D)), gate=gt,
+                        gate_stride=cfg.D if gt is not None else None, out=out)
+        torch.cuda.synchronize()
+        c.close()
+
+
 def bench_c1(torch, E, W, steps, warmup):
     cfg = W.C1
     q, k, v, _ = W.decode_inputs(cfg, W.C1_PAST, seed=1)
@@ -279,6 +300,8 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline only (no extras, no CPU baseline)")
     ap.add_argument("--profile-loop", type=int, default=0,
                     help="run only the headline sweep this many times (for rocprofv3 --pmc), print nothing else")
+    ap.add_argument("--profile-prefill", type=int, default=0,
+                    help="run only the C2 and C5 prefill attention this many times each (for rocprofv3 --pmc)")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="run only a device-to-device copy of MIB MiB (3 times) to calibrate the "
@@ -305,6 +328,10 @@ def main():
         for _ in range(3):
             b.copy_(a)
         torch.cuda.synchronize()
+        return
+
+    if args.profile_prefill:
+        profile_prefill(torch, E, W, args.profile_prefill)
         return
 
     L = 32768
