@@ -33,6 +33,12 @@ SIGNATURES = [
     ("bg_evict_plan", _i32, [_i32, _i32, _i32, _i32, _pi32, _pi32, _pi32]),
     ("bg_ring_map", _i32, [_i32, _i32, _i32, _i32, _pi32]),
     ("bg_stream_sync", _i32, [_vp]),
+    ("bg_stream_create", _i32, [C.POINTER(_vp)]),
+    ("bg_stream_destroy", _i32, [_vp]),
+    ("bg_event_create", _i32, [C.POINTER(_vp)]),
+    ("bg_event_record", _i32, [_vp, _vp]),
+    ("bg_event_elapsed_us", _i32, [_vp, _vp, C.POINTER(_f32)]),
+    ("bg_event_destroy", _i32, [_vp]),
     ("bg_kv_create", _i32, [_i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, C.POINTER(_vp)]),
     ("bg_kv_destroy", _i32, [_vp]),
     ("bg_kv_capacity", _i32, [_vp, _pi32]),

@@ -180,6 +180,55 @@ int32_t bg_stream_sync(void* stream) {
   return e == hipSuccess ? BG_OK : hip_fail(e, "stream sync");
 }
 
+int32_t bg_stream_create(void** stream) {
+  if (!stream) return fail(BG_E_INVALID, "bg_stream_create: out is NULL");
+  *stream = nullptr;
+  hipStream_t s;
+  hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);  // default priority
+  if (e != hipSuccess) return hip_fail(e, "stream create");
+  *stream = (void*)s;
+  return BG_OK;
+}
+
+int32_t bg_stream_destroy(void* stream) {
+  if (!stream) return BG_OK;
+  hipError_t e = hipStreamDestroy((hipStream_t)stream);
+  return e == hipSuccess ? BG_OK : hip_fail(e, "stream destroy");
+}
+
+int32_t bg_event_create(void** event) {
+  if (!event) return fail(BG_E_INVALID, "bg_event_create: out is NULL");
+  *event = nullptr;
+  hipEvent_t ev;
+  hipError_t e = hipEventCreate(&ev);
+  if (e != hipSuccess) return hip_fail(e, "event create");
+  *event = (void*)ev;
+  return BG_OK;
+}
+
+int32_t bg_event_record(void* event, void* stream) {
+  if (!event) return fail(BG_E_INVALID, "bg_event_record: event is NULL");
+  hipError_t e = hipEventRecord((hipEvent_t)event, (hipStream_t)stream);
+  return e == hipSuccess ? BG_OK : hip_fail(e, "event record");
+}
+
+int32_t bg_event_elapsed_us(void* start, void* end, float* us) {
+  if (!start || !end || !us) return fail(BG_E_INVALID, "bg_event_elapsed_us: NULL argument");
+  hipError_t e = hipEventSynchronize((hipEvent_t)end);
+  if (e != hipSuccess) return hip_fail(e, "event synchronize");
+  float ms = 0.0f;
+  e = hipEventElapsedTime(&ms, (hipEvent_t)start, (hipEvent_t)end);
+  if (e != hipSuccess) return hip_fail(e, "event elapsed time");
+  *us = ms * 1000.0f;
+  return BG_OK;
+}
+
+int32_t bg_event_destroy(void* event) {
+  if (!event) return BG_OK;
+  hipError_t e = hipEventDestroy((hipEvent_t)event);
+  return e == hipSuccess ? BG_OK : hip_fail(e, "event destroy");
+}
+
 int32_t bg_kv_create(int32_t n_layers, int32_t kv_heads, int32_t head_dim, int32_t dtype, int32_t capacity,
                      int32_t max_seq_len, int32_t roll, int32_t sinks, int32_t rope_pos_mode, bg_kv_cache** out) {
   if (!out) return fail(BG_E_INVALID, "bg_kv_create: out is NULL");

@@ -303,6 +303,44 @@ static napi_value js_sync(napi_env env, napi_callback_info info) {
   return NULL;
 }
 
+/* streamCreate() -> bigint; streamDestroy(stream); eventCreate() -> bigint;
+   eventRecord(event, stream); eventElapsedUs(start, end) -> number; eventDestroy(event) */
+static napi_value js_stream_create(napi_env env, napi_callback_info info) {
+  (void)info;
+  void* st = NULL;
+  RC(bg_stream_create(&st));
+  return ptr_value(env, st);
+}
+static napi_value js_stream_destroy(napi_env env, napi_callback_info info) {
+  ARGS(1);
+  RC(bg_stream_destroy(arg_ptr(env, a[0])));
+  return NULL;
+}
+static napi_value js_event_create(napi_env env, napi_callback_info info) {
+  (void)info;
+  void* ev = NULL;
+  RC(bg_event_create(&ev));
+  return ptr_value(env, ev);
+}
+static napi_value js_event_record(napi_env env, napi_callback_info info) {
+  ARGS(2);
+  RC(bg_event_record(arg_ptr(env, a[0]), arg_ptr(env, a[1])));
+  return NULL;
+}
+static napi_value js_event_elapsed_us(napi_env env, napi_callback_info info) {
+  ARGS(2);
+  float us = 0.0f;
+  RC(bg_event_elapsed_us(arg_ptr(env, a[0]), arg_ptr(env, a[1]), &us));
+  napi_value r;
+  napi_create_double(env, (double)us, &r);
+  return r;
+}
+static napi_value js_event_destroy(napi_env env, napi_callback_info info) {
+  ARGS(1);
+  RC(bg_event_destroy(arg_ptr(env, a[0])));
+  return NULL;
+}
+
 static napi_value init(napi_env env, napi_value exports) {
   napi_property_descriptor p[] = {
       {"version", 0, js_version, 0, 0, 0, napi_default, 0},
@@ -327,6 +365,12 @@ static napi_value init(napi_env env, napi_value exports) {
       {"h2d", 0, js_h2d, 0, 0, 0, napi_default, 0},
       {"d2h", 0, js_d2h, 0, 0, 0, napi_default, 0},
       {"sync", 0, js_sync, 0, 0, 0, napi_default, 0},
+      {"streamCreate", 0, js_stream_create, 0, 0, 0, napi_default, 0},
+      {"streamDestroy", 0, js_stream_destroy, 0, 0, 0, napi_default, 0},
+      {"eventCreate", 0, js_event_create, 0, 0, 0, napi_default, 0},
+      {"eventRecord", 0, js_event_record, 0, 0, 0, napi_default, 0},
+      {"eventElapsedUs", 0, js_event_elapsed_us, 0, 0, 0, napi_default, 0},
+      {"eventDestroy", 0, js_event_destroy, 0, 0, 0, napi_default, 0},
   };
   napi_define_properties(env, exports, sizeof(p) / sizeof(p[0]), p);
   return exports;

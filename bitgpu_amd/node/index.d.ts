@@ -26,3 +26,10 @@ export declare class KvCache {
   exportRows(li: number, region: 0 | 1 | 2 | 3, base: number, count: number): ArrayBuffer
   importRows(li: number, region: 0 | 1 | 2 | 3, base: number, count: number, buf: ArrayBuffer): void
 }
+// raw addon: streams (default priority) and event timing, for hosts without a GPU runtime
+export declare const addon: {
+  streamCreate(): DevPtr; streamDestroy(stream: DevPtr): void
+  eventCreate(): DevPtr; eventRecord(event: DevPtr, stream: DevPtr | null): void
+  eventElapsedUs(start: DevPtr, end: DevPtr): number; eventDestroy(event: DevPtr): void
+  [name: string]: any
+}

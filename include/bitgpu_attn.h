@@ -74,6 +74,19 @@ int32_t bg_ring_map(int32_t sinks, int32_t max_seq_len, int32_t head, int32_t lo
 /* Synchronize a stream (NULL = device). */
 int32_t bg_stream_sync(void* stream);
 
+/* ---- streams and event timing -------------------------------------------------------------
+ * For hosts without a GPU runtime of their own (the N-API addon): the reference runs every
+ * dispatch on its one WebGPU queue and times with timestamp queries (src/engine.ts:503-506);
+ * here a stream is that queue (default priority; NULL = the null stream in every call) and
+ * two recorded events give the elapsed time between them (bg_event_elapsed_us waits for
+ * `end`). */
+int32_t bg_stream_create(void** stream);
+int32_t bg_stream_destroy(void* stream);
+int32_t bg_event_create(void** event);
+int32_t bg_event_record(void* event, void* stream);
+int32_t bg_event_elapsed_us(void* start, void* end, float* us);
+int32_t bg_event_destroy(void* event);
+
 /* ---- KV cache lifecycle ------------------------------------------------------------------
  * Replaces the Kc/Vc/Ksc/Vsc allocation of src/engine.ts:1044-1079, the kvCache/overflow/
  * sinkTokens/maxSeqLen options (src/types.ts:138-177) and the roll statics (1094-1111). */

@@ -156,3 +156,37 @@ def test_argument_errors_are_raised_not_faulted(dev):
     with pytest.raises(BitgpuError, match="beyond capacity"):
         c.append_kv(t(np.zeros((8, 128), np.float32)), BG_K, 0, 8, 64 * 8)
     c.close()
+
+
+def test_stream_and_event_utilities(dev):
+    """bg_stream_create / bg_event_*: the same attention launched on a library-created stream
+    (timed by two events recorded on it) and on torch's stream gives identical bytes."""
+    import ctypes as C
+    from bitgpu_amd import _lib
+    lib = _lib.lib()
+    st, e0, e1 = C.c_void_p(), C.c_void_p(), C.c_void_p()
+    _lib.check(lib.bg_stream_create(C.byref(st)))
+    _lib.check(lib.bg_event_create(C.byref(e0)))
+    _lib.check(lib.bg_event_create(C.byref(e1)))
+    rng = np.random.default_rng(11)
+    L, H, KV, D = 2000, 32, 8, 128
+    k = rng.standard_normal((L, KV, D)).astype(np.float32)
+    v = rng.standard_normal((L, KV, D)).astype(np.float32)
+    q = t(rng.standard_normal((1, H, D)).astype(np.float32))
+    c = E.KvCache(1, KV, D, "q8", max_seq_len=L, capacity=L)
+    fill_cache_raw(c, 0, k, v)
+    ref_out = E.attention(c, 0, q, 1, H, L - 1)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(torch.cuda.ExternalStream(st.value)):
+        _lib.check(lib.bg_event_record(e0, st))
+        out = E.attention(c, 0, q, 1, H, L - 1)
+        _lib.check(lib.bg_event_record(e1, st))
+    us = C.c_float()
+    _lib.check(lib.bg_event_elapsed_us(e0, e1, C.byref(us)))
+    _lib.check(lib.bg_stream_sync(st))
+    assert 0.0 < us.value < 1e6
+    assert torch.equal(out, ref_out)
+    for ev in (e0, e1):
+        _lib.check(lib.bg_event_destroy(ev))
+    _lib.check(lib.bg_stream_destroy(st))
+    c.close()

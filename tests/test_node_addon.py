@@ -61,7 +61,7 @@ def test_addon_attention_on_gpu(tmp_path, dtype, S):
     q = rng.standard_normal((S, H, D)).astype(np.float32)
     for name, arr in (("k", k), ("v", v), ("q", q)):
         arr.tofile(tmp_path / f"{name}.bin")
-    run_node(f"""
+    _ = run_node(f"""
 const fs = require('fs')
 const rd = n => {{ const b = fs.readFileSync({json.dumps(str(tmp_path))} + '/' + n + '.bin'); return new Float32Array(b.buffer, b.byteOffset, b.length / 4) }}
 const a = b.addon
@@ -71,13 +71,21 @@ a.h2d(dk, k); a.h2d(dv, v); a.h2d(dq, q)
 const c = new b.KvCache({{layers: 2, kvHeads: {KV}, headDim: {D}, kvCache: '{dtype}', maxSeqLen: 512, capacity: {L}}})
 c.appendKV(dk, b.K, 1, {L * KV}, 0)
 c.appendKV(dv, b.V, 1, {L * KV}, 0)
-c.att(dq, 1, {S}, {H}, {L - S}, dout)
+const st = a.streamCreate(), e0 = a.eventCreate(), e1 = a.eventCreate()
+a.eventRecord(e0, st)
+c.att(dq, 1, {S}, {H}, {L - S}, dout, {{stream: st}})
+a.eventRecord(e1, st)
+const us = a.eventElapsedUs(e0, e1)
 a.sync()
 const out = new Float32Array(q.length)
 a.d2h(out, dout)
 fs.writeFileSync({json.dumps(str(tmp_path))} + '/out.bin', Buffer.from(out.buffer))
+a.eventDestroy(e0); a.eventDestroy(e1); a.streamDestroy(st)
 c.dispose()
+console.log(JSON.stringify({{us}}))
 """, tmp_path)
+    us = json.loads(_.strip().splitlines()[-1])["us"]
+    assert 0.0 < us < 1e6  # the attention ran on the addon's own stream, timed by its events
     out = np.fromfile(tmp_path / "out.bin", np.float32).reshape(S, H, D)
     exp = ref.attention(q, ref.kv_roundtrip(k, dtype), ref.kv_roundtrip(v, dtype), L - S)
     assert np.abs(out - exp).max() / np.abs(exp).max() <= 2e-3
