@@ -450,9 +450,12 @@ __global__ __launch_bounds__(256 * TEAMS) void prefill_kernel(PrefillParams p) {
       const bool live = s < my_count;
       const int j0 = (my_first + (live ? s : 0)) * KT;
       // S^T = K Q^T
-      floatx16 sacc[NSUB];
+      // one 32-key sub-tile (D=256): two accumulators over even / odd dim chunks, so the QK
+      // MFMAs form two independent chains
+      constexpr int NA = NSUB == 1 ? 2 : NSUB;
+      floatx16 sacc[NA];
 #pragma unroll
-      for (int u = 0; u < NSUB; u++)
+      for (int u = 0; u < NA; u++)
 #pragma unroll
         for (int e = 0; e < 16; e++) sacc[u][e] = 0.0f;
 #pragma unroll
@@ -461,8 +464,10 @@ __global__ __launch_bounds__(256 * TEAMS) void prefill_kernel(PrefillParams p) {
         for (int u = 0; u < NSUB; u++) {
           PH8 a;
           a.u = ldv(kc + k_chunk_pos<D>(u * 32 + n, 2 * c + g2) * 8);
-          sacc[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a.h, qf[c], sacc[u], 0, 0, 0);
+          const int acc = NSUB == 1 ? (c & 1) : u;
+          sacc[acc] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a.h, qf[c], sacc[acc], 0, 0, 0);
         }
+      if constexpr (NSUB == 1) sacc[0] += sacc[1];
       // mask + online softmax (row = this lane's n)
       float x[NSUB][16];
       float mt = -INFINITY;
