@@ -19,6 +19,7 @@
 // (tools/reference.py:107) and y*cos + rot*sin as two rounded products and a rounded sum
 // (tools/reference.py:149-152; shaders/rmsnorm_rope_sg.wgsl:32), no FMA contraction.
 #include "bg_kernels.h"
+#include "bg_row.h"
 #include "bg_store.h"
 
 namespace bg {
@@ -103,7 +104,7 @@ __global__ __launch_bounds__(256) void qkv_prologue_kernel(LayerView L, Prologue
   const int nqk_items = (nqk + NR - 1) / NR;
   if (item < nqk_items) {
     // ---------------- NR Q/K rows: RMSNorm (+ RoPE); every load issued before any compute ----------------
-    const int rot = a.rot_dim, half = rot >> 1;
+    const int rot = a.rot_dim;
     float v[NR][EPL], cs[NR][EPL], sn[NR][EPL];
 #pragma unroll
     for (int j = 0; j < NR; j++) {
@@ -121,49 +122,17 @@ __global__ __launch_bounds__(256) void qkv_prologue_kernel(LayerView L, Prologue
 #pragma unroll
       for (int e = 0; e < EPL; e++) v[j][e] = x[d0 + e];
       // table rows only for rows that rotate (the range is validated only for those)
-      const bool rope_j = isq || gr.rope_k;
-      const int p = a.pos0 + s;
-#pragma unroll
-      for (int e = 0; e < EPL; e++) {
-        const int d = d0 + e;
-        const int ti = d < rot ? (d < half ? d : d - half) : 0;
-        cs[j][e] = rope_j ? a.cos_tab[(size_t)p * half + ti] : 0.0f;
-        sn[j][e] = rope_j ? a.sin_tab[(size_t)p * half + ti] : 0.0f;
-      }
+      rope_entries<D>(a.cos_tab, a.sin_tab, a.pos0 + s, rot, isq || gr.rope_k, cs[j], sn[j], lane);
     }
 #pragma unroll
     for (int j = 0; j < NR; j++) {
       const int r = item * NR + j;
       const bool isq = r < gr.nq;
       const bool rope = isq || gr.rope_k;
-      float ss = 0.0f;
-#pragma unroll
-      for (int e = 0; e < EPL; e++) ss = __fadd_rn(ss, __fmul_rn(v[j][e], v[j][e]));
-      ss = wave_sum(ss);
-      const float rms = __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)D), a.eps));
-      const float* g = isq ? a.q_gamma : a.k_gamma;
       float y[EPL];
 #pragma unroll
-      for (int e = 0; e < EPL; e++) y[e] = __fmul_rn(__fdiv_rn(v[j][e], rms), g[d0 + e]);
-      if (rope) {
-        float* row = rowbuf[wave];
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();  // the previous row's partner reads are done
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-        for (int e = 0; e < EPL; e++) row[d0 + e] = y[e];
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-        for (int e = 0; e < EPL; e++) {
-          const int d = d0 + e;
-          if (d < rot) {
-            const float rv = d < half ? -row[d + half] : row[d - half];
-            y[e] = __fadd_rn(__fmul_rn(y[e], cs[j][e]), __fmul_rn(rv, sn[j][e]));
-          }
-        }
-      }
+      for (int e = 0; e < EPL; e++) y[e] = v[j][e];
+      rmsnorm_rope_wave<D>(y, isq ? a.q_gamma : a.k_gamma, a.eps, rope, rot, cs[j], sn[j], rowbuf[wave], lane);
       if (r < nqk) {
         if (isq) {
           float* o = a.q_out + (size_t)r * D;  // r = s * H + head
