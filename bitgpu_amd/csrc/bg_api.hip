@@ -455,6 +455,9 @@ static int32_t ensure_workspace(bg_kv_cache* c, int S, int H) {
   hipError_t e = hipMalloc((void**)&c->ws, need * sizeof(float));
   if (e == hipSuccess) e = hipMalloc((void**)&c->ws_count, counters * sizeof(unsigned));
   if (e == hipSuccess) e = hipMemset(c->ws_count, 0, counters * sizeof(unsigned));
+  // decode split slots start out "empty"; every decode launch leaves them that way
+  if (e == hipSuccess) e = hipMemsetD32((hipDeviceptr_t)c->ws, (int)bg::decode_workspace_empty(), need);
+  if (e == hipSuccess) e = hipDeviceSynchronize();
   if (e != hipSuccess) {
     if (c->ws) (void)hipFree(c->ws);
     if (c->ws_count) (void)hipFree(c->ws_count);

@@ -65,8 +65,10 @@ bool f32_split_supported(const LayerView& L, int S, int H);
 size_t f32_workspace_floats(const LayerView& L, int S, int H);
 hipError_t launch_attention_decode(const LayerView& L, const AttnArgs& a, hipStream_t st);
 hipError_t launch_attention_prefill(const LayerView& L, const AttnArgs& a, hipStream_t st);
-// workspace floats needed by the decode kernel for S rows of H heads
+// workspace floats needed by the decode kernel for S rows of H heads; a new workspace is filled
+// with the 32-bit pattern decode_workspace_empty() before its first use
 size_t decode_workspace_floats(const LayerView& L, int S, int H, int num_cus, size_t* counters);
+uint32_t decode_workspace_empty();
 bool decode_supported(const LayerView& L, int S, int H);
 bool prefill_supported(const LayerView& L, int S, int H);
 

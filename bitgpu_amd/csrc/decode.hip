@@ -4,8 +4,8 @@
 // S<=12): those run one subgroup per (query, head) scanning every position serially
 // (attention_sg.wgsl:31-42). Here the context is split across all CUs:
 //
-//   grid  = n_splits x KV workgroups, 4 waves each; a workgroup owns one kv head and a range of
-//           32-slot tiles; its waves take every 4th tile. All R = (H/KV)*S query rows of the
+//   grid  = n_splits x KV workgroups, NW = 4 or 8 waves each; a workgroup owns one kv head and
+//           a range of 32-slot tiles; its waves take every NW-th tile. All R = (H/KV)*S query rows of the
 //           GQA group are served by one read of each K/V byte.
 //   QK    = v_mfma_f32_16x16x32_f16 with K as the B operand (lane = slot, 8 dims per lane
 //           group) and a block-diagonal Q as A: row group g of the 16 output rows only sees the
@@ -18,9 +18,10 @@
 //           through a 2 KB-per-block LDS transpose into the B operand of
 //   PV    = v_mfma_f32_16x16x32_f16 with V^T (the cache's transposed V tile, 16 B per lane)
 //           as A and P^T as B.
-//   merge = the 4 waves combine through LDS; splits write (m, l, o) partials and the last
-//           workgroup of each kv head (atomic ticket) does the log-sum-exp merge, the output
-//           gate (gate_sigmoid.wgsl:13) and the store -- one launch per layer.
+//   merge = the waves combine through LDS; splits write (m, l, o) partials and a per-split
+//           flag stamped with the launch epoch; the first splits of each kv head poll the
+//           flags and each does the log-sum-exp merge, the output gate (gate_sigmoid.wgsl:13)
+//           and the store for its (row, 64-dim) units -- one launch per layer.
 // Sink mode reads unroped K and rotates it at read by the slot's logical (or absolute) position
 // (attention_sg_roll.wgsl:40-51), in f32 before the f16 conversion.
 #include "bg_kernels.h"
@@ -58,7 +59,17 @@ __device__ inline half8 q8_to_half8(uint32_t w0, uint32_t w1) {
 
 __device__ inline float code_of(uint32_t w, int byte) { return (float)(int8_t)(w >> (8 * byte)); }
 
-__device__ inline uint4 ld16(const void* p) { return *(const uint4*)p; }
+// K/V tile bytes are read once per launch: nontemporal loads (streaming cache policy) keep them
+// from displacing reusable lines and sustain a higher HBM rate than plain loads.
+__device__ inline uint4 ld16(const void* p) {
+  const u32x4v v = __builtin_nontemporal_load((const u32x4v*)p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ inline float ldnt(const float* p) { return __builtin_nontemporal_load(p); }
+__device__ inline float4 ldnt4(const float* p) {
+  const floatx4 v = __builtin_nontemporal_load((const floatx4*)p);
+  return make_float4(v[0], v[1], v[2], v[3]);
+}
 
 
 // which dims lane group g feeds into QK MFMA #t (element e = 0..7 of the lane's half8)
@@ -84,11 +95,19 @@ struct DecodeParams {
   int n_scan;        // physical slots to scan
   int phys_limit;    // physical slots that can hold data
   int n_tiles, tiles_per_split, n_splits;
-  float* ws_o;       // [KV][n_splits][R][D]
-  float* ws_ml;      // [KV][n_splits][R][2]
-  unsigned* ws_count;  // [KV]
-  int merge_ext;     // 1: the splits only publish; decode_merge_kernel merges after this launch
+  // split partials, [KV][units][n_splits][17] float4 with unit = (row, 64-dim chunk): 16 float4
+  // of o, then (m, l, -, -). Every slot holds kPartialEmpty except between a split's store and
+  // the merger's read of it in the same launch.
+  float4* ws;
+  int n_mergers;       // splits 0 .. n_mergers-1 also merge units u = split, split + n_mergers, ..
 };
+
+// "not written yet" marker of a partial slot: a quiet NaN with a payload that arithmetic on
+// finite inputs never produces
+constexpr uint32_t kPartialEmpty = 0x7FF1DE5Au;
+constexpr int kUnitF4 = 17;  // float4 per (unit, split) slot
+// splits per kv head at most (the merge holds a column of every split in registers)
+constexpr int kMaxSplits = 256;
 
 // Shared memory plan (bytes): Q operands, per-wave P^T tiles, per-wave corr; after the tile
 // loop the same space holds the per-wave partials, then the split merge's weights and sums.
@@ -124,10 +143,12 @@ struct TileRegs {
   float vsc[2][DT == KV_Q8 ? NB : 1];
 };
 
+// The K part of a tile's loads (K codes and both scale rows: the V scales are folded into the
+// probabilities) and the V part are issued separately, so each can be re-issued for a later tile
+// as soon as its phase of the current tile has consumed it.
 template <int D, int DT, bool QUARTER>
-__device__ __forceinline__ void load_tile(TileRegs<D, DT, QUARTER>& T, int j0, int g, int n,
-                                          const unsigned char* kbase, const unsigned char* vbase,
-                                          const float* ksb, const float* vsb) {
+__device__ __forceinline__ void load_tile_k(TileRegs<D, DT, QUARTER>& T, int j0, int g, int n,
+                                            const unsigned char* kbase, const float* ksb, const float* vsb) {
   constexpr int NB = D / 32;
   constexpr int KU = TileRegs<D, DT, QUARTER>::KU;
   constexpr int NSUB = QUARTER ? (D / 128) : 1;
@@ -140,7 +161,7 @@ __device__ __forceinline__ void load_tile(TileRegs<D, DT, QUARTER>& T, int j0, i
 #pragma unroll
       for (int i = 0; i < KU; i++) T.kr[t2][i] = ld16(row + g * (D / 4) + 16 * i);
 #pragma unroll
-      for (int i = 0; i < NSUB; i++) T.ksc[t2][i] = ksb[(size_t)P * NB + g * NSUB + i];
+      for (int i = 0; i < NSUB; i++) T.ksc[t2][i] = ldnt(ksb + (size_t)P * NB + g * NSUB + i);
     } else {
       constexpr int HU = KU / 2;  // uint4 per half piece
 #pragma unroll
@@ -149,14 +170,14 @@ __device__ __forceinline__ void load_tile(TileRegs<D, DT, QUARTER>& T, int j0, i
         T.kr[t2][HU + i] = ld16(row + (D / 2 + g * (D / 8)) * eb + 16 * i);
       }
       if constexpr (DT == KV_Q8) {
-        T.ksc[t2][0] = ksb[(size_t)P * NB + (g * (D / 8)) / 32];
-        T.ksc[t2][1] = ksb[(size_t)P * NB + (D / 2 + g * (D / 8)) / 32];
+        T.ksc[t2][0] = ldnt(ksb + (size_t)P * NB + (g * (D / 8)) / 32);
+        T.ksc[t2][1] = ldnt(ksb + (size_t)P * NB + (D / 2 + g * (D / 8)) / 32);
       }
     }
     if constexpr (DT == KV_Q8) {
 #pragma unroll
       for (int b = 0; b < NB; b += 4) {
-        const float4 f = *(const float4*)(vsb + (size_t)P * NB + b);
+        const float4 f = ldnt4(vsb + (size_t)P * NB + b);
         T.vsc[t2][b] = f.x;
         T.vsc[t2][b + 1] = f.y;
         T.vsc[t2][b + 2] = f.z;
@@ -164,6 +185,13 @@ __device__ __forceinline__ void load_tile(TileRegs<D, DT, QUARTER>& T, int j0, i
       }
     }
   }
+}
+
+template <int D, int DT, bool QUARTER>
+__device__ __forceinline__ void load_tile_v(TileRegs<D, DT, QUARTER>& T, int j0, int g, int n,
+                                            const unsigned char* vbase) {
+  constexpr int NB = D / 32;
+  constexpr size_t eb = (DT == KV_Q8) ? 1 : 2;
   const unsigned char* vt = vbase + ((size_t)j0 * D + (size_t)g * 8 * D) * eb;
 #pragma unroll
   for (int b = 0; b < NB; b++) {
@@ -174,6 +202,14 @@ __device__ __forceinline__ void load_tile(TileRegs<D, DT, QUARTER>& T, int j0, i
       T.vr[2 * b + 1] = ld16(vt + (size_t)(32 * b + 2 * n) * 16 + 16);
     }
   }
+}
+
+template <int D, int DT, bool QUARTER>
+__device__ __forceinline__ void load_tile(TileRegs<D, DT, QUARTER>& T, int j0, int g, int n,
+                                          const unsigned char* kbase, const unsigned char* vbase,
+                                          const float* ksb, const float* vsb) {
+  load_tile_k<D, DT, QUARTER>(T, j0, g, n, kbase, ksb, vsb);
+  load_tile_v<D, DT, QUARTER>(T, j0, g, n, vbase);
 }
 
 template <int D, int DT, bool ROLL, int NSET, int NW>
@@ -190,7 +226,10 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
 
   extern __shared__ __align__(16) unsigned char smem[];
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  // wave-uniform (scalar) so the tile loop's trip count is uniform control flow: with a
+  // divergent one the loop becomes exec-masked flow and the tile prefetch is waited for at the
+  // loop head instead of staying in flight
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int g = lane >> 4;      // lane group
   const int n = lane & 15;
@@ -216,8 +255,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
 
   // Q operands (block diagonal, hi/lo f16). The setup is straight-line code -- every load is
   // unconditional (spare slots read query 0, a wave without tiles re-reads the split's last
-  // tile) and spare slots store to a sink -- so the q gather, issued first, can be waited for
-  // on its own while the first tile's loads stay in flight.
+  // tile) and spare slots store to a sink.
   TileRegs<D, DT, QUARTER> A, B;
   const int tile0 = t_begin + wave;
   {
@@ -238,9 +276,6 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
       qv[i][0] = a.x; qv[i][1] = a.y; qv[i][2] = a.z; qv[i][3] = a.w;
       qv[i][4] = b.x; qv[i][5] = b.y; qv[i][6] = b.z; qv[i][7] = b.w;
     }
-    const int ta = tile0 < t_end ? tile0 : t_end - 1;
-    load_tile<D, DT, QUARTER>(A, ta * 32, g, n, kbase, vbase, ksb, vsb);
-    __builtin_amdgcn_sched_barrier(0);  // every load above is issued before the first wait
 #pragma unroll
     for (int i = 0; i < QMAX; i++) {
       const int idx = i * NTHR + tid;
@@ -258,6 +293,12 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
       qs[o0] = hi.u;
       qs[o1] = lo.u;
     }
+    // The first tile is issued only once q has arrived: q issued alone returns in ~0.3 us, while
+    // behind every CU's first tile (~19 MB queued at once) it returns only after them. The
+    // scheduling barrier keeps the compiler from hoisting the tile loads above the q stores.
+    __builtin_amdgcn_sched_barrier(0);
+    const int ta = tile0 < t_end ? tile0 : t_end - 1;
+    load_tile<D, DT, QUARTER>(A, ta * 32, g, n, kbase, vbase, ksb, vsb);
   }
   // zero this wave's P tiles (rows never written stay zero) and set corr = 1
   {
@@ -276,7 +317,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
 #pragma unroll
     for (int i = 0; i < D / 16; i++) o[s][i] = floatx4{0, 0, 0, 0};
 
-  auto process = [&](const TileRegs<D, DT, QUARTER>& T, int tile) {
+  auto qk_softmax = [&](const TileRegs<D, DT, QUARTER>& T, int tile) {
     const int j0 = tile * 32;
     // ---------------- K operands ----------------
     // K operand for QK MFMA t of 16-slot group t2: converted just in time (plain cache) or
@@ -394,7 +435,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
 #pragma unroll
       for (int t2 = 0; t2 < 2; t2++) {
         const int P = j0 + 16 * t2 + n;
-        const int Lg = ring.logical(P);
+        const int Lg = ROLL ? ring.logical(P) : P;  // a plain cache is never a ring
         const bool ok = row_ok && P < p.n_scan && P < p.phys_limit && Lg <= limit;
         x[t2] = ok ? sc[t2] : -INFINITY;
       }
@@ -422,8 +463,10 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
 
-    // ---------------- PV ----------------
+  // ---------------- PV ----------------
+  auto pv = [&](const TileRegs<D, DT, QUARTER>& T) {
     auto vop = [&](int b, int par) -> half8 {
       if constexpr (DT == KV_Q8) {
         return par ? q8_to_half8(T.vr[b].z, T.vr[b].w) : q8_to_half8(T.vr[b].x, T.vr[b].y);
@@ -451,17 +494,64 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   };
 
-  // software pipeline: the next tile's loads are in flight while this one computes. The
-  // prefetch is unconditional (past the end it re-reads the current, cached tile) so the
-  // compiler can count outstanding loads instead of draining them every tile.
-  for (int tile = tile0; tile < t_end; tile += 2 * NW) {
-    const int t1 = tile + NW < t_end ? tile + NW : tile;
-    load_tile<D, DT, QUARTER>(B, t1 * 32, g, n, kbase, vbase, ksb, vsb);
-    process(A, tile);
-    if (tile + NW >= t_end) break;
-    const int t2n = tile + 2 * NW < t_end ? tile + 2 * NW : tile + NW;
-    load_tile<D, DT, QUARTER>(A, t2n * 32, g, n, kbase, vbase, ksb, vsb);
-    process(B, tile + NW);
+  // software pipeline over this wave's tiles (every NW-th tile from tile0): two tiles are in
+  // flight. For q8 each phase's registers are re-issued for the tile two ahead as soon as that
+  // phase of the current tile is done (K part after QK + softmax, V part after PV), so the memory
+  // queue refills while the rest of the tile computes. The loop bodies' loads are unconditional
+  // and there is no early exit, so every path into a loop head has the same loads outstanding
+  // and the compiler counts them instead of draining them.
+  const int nmy = tile0 < t_end ? (t_end - tile0 + NW - 1) / NW : 0;  // this wave's tiles
+  int it = 0;
+  if constexpr (DT == KV_Q8) {
+    {
+      const int tb = nmy > 1 ? tile0 + NW : (tile0 < t_end ? tile0 : t_end - 1);
+      load_tile<D, DT, QUARTER>(B, tb * 32, g, n, kbase, vbase, ksb, vsb);
+    }
+    for (; it + 4 <= nmy; it += 2) {
+      const int ta = tile0 + it * NW;
+      qk_softmax(A, ta);
+      load_tile_k<D, DT, QUARTER>(A, (ta + 2 * NW) * 32, g, n, kbase, ksb, vsb);
+      pv(A);
+      load_tile_v<D, DT, QUARTER>(A, (ta + 2 * NW) * 32, g, n, vbase);
+      qk_softmax(B, ta + NW);
+      load_tile_k<D, DT, QUARTER>(B, (ta + 3 * NW) * 32, g, n, kbase, ksb, vsb);
+      pv(B);
+      load_tile_v<D, DT, QUARTER>(B, (ta + 3 * NW) * 32, g, n, vbase);
+    }
+    // the last one to three tiles: A and B hold tiles it and it + 1
+    const int r = nmy - it;
+    const int ta = tile0 + it * NW;
+    if (r >= 1) {
+      qk_softmax(A, ta);
+      pv(A);
+    }
+    if (r == 3) load_tile<D, DT, QUARTER>(A, (ta + 2 * NW) * 32, g, n, kbase, vbase, ksb, vsb);
+    if (r >= 2) {
+      qk_softmax(B, ta + NW);
+      pv(B);
+    }
+    if (r == 3) {
+      qk_softmax(A, ta + 2 * NW);
+      pv(A);
+    }
+  } else {
+    // f16 tiles are twice as large: the registers hold two whole tiles, so the next tile is
+    // issued before a tile is processed and re-issued only after both of its phases (past the
+    // end the prefetch re-reads the tile just loaded, still cached)
+    for (; it + 2 <= nmy; it += 2) {
+      const int ta = tile0 + it * NW;
+      load_tile<D, DT, QUARTER>(B, (ta + NW) * 32, g, n, kbase, vbase, ksb, vsb);
+      qk_softmax(A, ta);
+      pv(A);
+      const int tn = it + 2 < nmy ? ta + 2 * NW : ta + NW;
+      load_tile<D, DT, QUARTER>(A, tn * 32, g, n, kbase, vbase, ksb, vsb);
+      qk_softmax(B, ta + NW);
+      pv(B);
+    }
+    if (it < nmy) {
+      qk_softmax(A, tile0 + it * NW);
+      pv(A);
+    }
   }
 
   // ---------------- combine the waves of the workgroup ----------------
@@ -513,10 +603,12 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
 
   const bool single = p.n_splits == 1;
   constexpr int kSC1 = 16;  // cache policy sc1: agent-coherent (written through / read from memory)
+  constexpr int UPR = D / 64;  // merge units per row
   const int C4 = p.R * (D / 4);
-  float* wso = single ? p.out : p.ws_o + ((size_t)kvh * p.n_splits + split) * p.R * D;
-  float* wsml = single ? p.out : p.ws_ml + ((size_t)kvh * p.n_splits + split) * p.R * 2;
-  const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc((void*)wso, (short)0, 0x7fffffff, 0x00020000);
+  const int NS = p.n_splits;
+  const int units = p.R * UPR;
+  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.ws + (size_t)kvh * units * NS * kUnitF4), (short)0, 0x7fffffff, 0x00020000);
   for (int c = tid; c < C4; c += NTHR) {
     const int rho = c / (D / 4), d = 4 * (c % (D / 4));
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -539,160 +631,132 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
         for (int e = 0; e < 4; e++) r[e] = r[e] / (1.0f + expf(-gr[e]));
       }
       *(float4*)(p.out + ((size_t)s * p.H + h) * D + d) = make_float4(r[0], r[1], r[2], r[3]);
-    } else if (p.merge_ext) {  // read by the next launch: plain stores
-      *(float4*)(wso + rho * D + d) = acc;
-      if (d == 0) *(float2*)&wsml[2 * rho] = make_float2(row_max(rho), lt);
     } else {
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4v, acc), ors, (rho * D + d) * 4, 0, kSC1);
-      if (d == 0) st_coherent2(&wsml[2 * rho], row_max(rho), lt);
-    }
-  }
-  if (single || p.merge_ext) return;
-
-  // ---------------- last workgroup of this kv head merges the splits ----------------
-  __shared__ unsigned s_last;
-  wait_stores();
-  __syncthreads();
-  if (tid == 0) {
-    const unsigned prev = __hip_atomic_fetch_add(&p.ws_count[kvh], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = (prev == (unsigned)(p.n_splits - 1)) ? 1u : 0u;
-  }
-  __syncthreads();
-  if (!s_last) return;
-  // Coherent reads of the other workgroups' partials: buffer loads with the sc1 cache policy --
-  // ordinary loads to the compiler, so a batch stays in flight.
-  const int NS = p.n_splits;
-  const int R = p.R;
-  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(p.ws_o + (size_t)kvh * NS * R * D), (short)0, 0x7fffffff, 0x00020000);
-  const __amdgpu_buffer_rsrc_t mrs = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(p.ws_ml + (size_t)kvh * NS * R * 2), (short)0, 0x7fffffff, 0x00020000);
-  // partial float4 loads in flight per thread (D=256 partials are twice as long and its four
-  // waves have a full SIMD's registers after the tile loop)
-  constexpr int MAXL = D == 128 ? 8 : 16;
-  const int TPC = NTHR >= C4 ? NTHR / C4 : 1;  // threads per float4 column
-  const int CPT = NTHR / TPC;                  // columns per pass
-  float* wts = (float*)smem;                   // [NS][R] merge weights
-  float* mls = wts + NS * R;                   // [NS][R][2] (split lists longer than a wave)
-  float4* red = (float4*)(mls + 2 * NS * R);   // [TPC][CPT] partial sums
-  // (1) (m, l) of the splits. Up to 64 splits: a wave takes a row, one split per lane, in
-  // registers. Issued first and unconditionally (indices clamped), so waiting for them does not
-  // wait for the partials behind them.
-  constexpr int RPW = (RS + NW - 1) / NW;      // rows per wave
-  const bool lane_split = NS <= 64;
-  uint2 mlv[RPW];
-#pragma unroll
-  for (int k = 0; k < RPW; k++) {
-    const int rho = min(wave + k * NW, R - 1);
-    const int sp = min(lane, NS - 1);
-    mlv[k] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(mrs, (sp * R + rho) * 8, 0, kSC1));
-  }
-  floatx4 pre[MAXL];
-  {
-    const int c = tid % CPT, k = tid / CPT;
-    const bool act = c < C4 && k < TPC;
-    // branch-free (an out-of-range split re-reads the last one and gets weight 0), so all loads
-    // of a batch stay in flight together
-#pragma unroll
-    for (int i = 0; i < MAXL; i++) {
-      const int sp = min(k + TPC * i, NS - 1);
-      const int cc = act ? c : 0;
-      pre[i] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(wrs, (sp * R * D + 4 * cc) * 4, 0, kSC1));
-    }
-  }
-  // (2) weights w[sp][rho] = 2^(m_sp - M) / sum_sp l_sp 2^(m_sp - M)
-  if (lane_split) {
-#pragma unroll
-    for (int k = 0; k < RPW; k++) {
-      const int rho = wave + k * NW;
-      if (rho < R) {
-        const bool ok = lane < NS;
-        const float mi = ok ? __uint_as_float(mlv[k].x) : -INFINITY;
-        const float li = ok ? __uint_as_float(mlv[k].y) : 0.0f;
-        const float M = wave_max(mi);
-        const float e = __builtin_amdgcn_exp2f(mi - M);
-        const float lt = wave_sum(li * e);
-        if (ok) wts[lane * R + rho] = e / lt;
+      const int slot = ((rho * UPR + d / 64) * NS + split) * kUnitF4;
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4v, acc), wrs, (slot + (d % 64) / 4) * 16, 0, kSC1);
+      if (d % 64 == 0) {
+        const float4 ml = make_float4(row_max(rho), lt, 0.0f, 0.0f);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4v, ml), wrs, (slot + 16) * 16, 0, kSC1);
       }
     }
-  } else {
-    for (int i = tid; i < NS * R; i += NTHR) {
-      const uint2 u = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(mrs, i * 8, 0, kSC1));
-      mls[2 * i] = __uint_as_float(u.x);
-      mls[2 * i + 1] = __uint_as_float(u.y);
-    }
-    __syncthreads();
-    for (int rho = wave; rho < R; rho += NW) {
-      float mx = -INFINITY;
-      for (int sp = lane; sp < NS; sp += 64) mx = fmaxf(mx, mls[2 * (sp * R + rho)]);
-      mx = wave_max(mx);
-      float lt = 0.0f;
-      for (int sp = lane; sp < NS; sp += 64) lt += mls[2 * (sp * R + rho) + 1] * __builtin_amdgcn_exp2f(mls[2 * (sp * R + rho)] - mx);
-      lt = wave_sum(lt);
-      for (int sp = lane; sp < NS; sp += 64) wts[sp * R + rho] = __builtin_amdgcn_exp2f(mls[2 * (sp * R + rho)] - mx) / lt;
-    }
   }
-  __syncthreads();
-  // (3) weighted sum of the partials, TPC threads per column, MAXL loads in flight per thread;
-  // with more than one batch the next is issued before the current one is consumed (loads past
-  // the last split re-read it and get weight 0)
-  const int BS = TPC * MAXL;  // splits per batch
-  for (int c0 = 0; c0 < C4; c0 += CPT) {
-    const int c = c0 + tid % CPT;
-    const int k = tid / CPT;
-    const bool act = c < C4 && k < TPC;
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (act) {
-      const int rho = (4 * c) / D;
-      auto issue = [&](floatx4 (&v)[MAXL], int b0) {
+  if (single || split >= p.n_mergers) return;
+
+  // ---------------- merge (splits 0 .. n_mergers-1) ----------------
+  // A merger polls its unit's slots of every split until none holds kPartialEmpty (the data
+  // itself is the completion signal: no flag, ticket or store acknowledgement to wait for), merges
+  // them by log-sum-exp, stores the output, and writes kPartialEmpty back for the next launch.
+  // Thread (k, c) holds float4 column c of splits k, k + KG, .. (MAXL at a time); wave 0 also
+  // holds (m, l) of every split, one per lane.
+  constexpr int KG = NTHR / 16;                // split groups
+  constexpr int MAXL = 4;                      // o slots per thread and batch
+  constexpr int MLC = (kMaxSplits + 63) / 64;  // (m, l) slots per lane of wave 0
+  const int c = tid & 15, k = tid >> 4;
+  float* wts = (float*)smem;                                   // [NS]
+  float4* red = (float4*)(smem + (((size_t)NS * 4 + 15) & ~(size_t)15));  // [NW][16]
+  const u32x4v empty4 = {kPartialEmpty, kPartialEmpty, kPartialEmpty, kPartialEmpty};
+  for (int u = split; u < units; u += p.n_mergers) {
+    const int rho = u / UPR, d0 = (u % UPR) * 64;
+    const int ubase = u * NS * kUnitF4;
+    floatx4 v[MAXL];
+    float2 ml[MLC];
+    // poll batch b0 of the o slots (wave 0 also the (m, l) slots) until nothing is missing;
+    // bounded: every split of the grid runs to completion on its own, so the data arrives, and
+    // the bound only guarantees an exit
+    auto poll = [&](int b0, bool with_ml) {
+      for (int it = 0; it < (1 << 20); it++) {
+        bool missing = false;
 #pragma unroll
         for (int i = 0; i < MAXL; i++) {
-          const int sp = min(b0 + k + TPC * i, NS - 1);
-          v[i] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(wrs, (sp * R * D + 4 * c) * 4, 0, kSC1));
+          const int sp = b0 + k + KG * i;
+          v[i] = sp < NS ? __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(wrs, (ubase + sp * kUnitF4 + c) * 16, 0, kSC1))
+                         : floatx4{0.f, 0.f, 0.f, 0.f};
         }
-      };
-      auto consume = [&](const floatx4 (&v)[MAXL], int b0) {
+        if (with_ml && wave == 0) {
 #pragma unroll
-        for (int i = 0; i < MAXL; i++) {
-          const int sp = b0 + k + TPC * i;
-          const float w = sp < NS ? wts[sp * R + rho] : 0.0f;
+          for (int j = 0; j < MLC; j++) {
+            const int sp = 64 * j + lane;
+            ml[j] = make_float2(-INFINITY, 0.0f);
+            if (64 * j < NS && sp < NS)
+              ml[j] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(wrs, (ubase + sp * kUnitF4 + 16) * 16, 0, kSC1));
+          }
+#pragma unroll
+          for (int j = 0; j < MLC; j++)
+            missing = missing || __float_as_uint(ml[j].x) == kPartialEmpty || __float_as_uint(ml[j].y) == kPartialEmpty;
+        }
+#pragma unroll
+        for (int i = 0; i < MAXL; i++)
+#pragma unroll
+          for (int e = 0; e < 4; e++) missing = missing || __float_as_uint(v[i][e]) == kPartialEmpty;
+        if (!__syncthreads_or(missing)) break;
+        __builtin_amdgcn_s_sleep(1);
+      }
+    };
+    // consume a batch: weighted sum, then mark its slots empty again
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    auto consume = [&](int b0) {
+#pragma unroll
+      for (int i = 0; i < MAXL; i++) {
+        const int sp = b0 + k + KG * i;
+        if (sp < NS) {
+          const float w = wts[sp];
           acc.x += v[i][0] * w;
           acc.y += v[i][1] * w;
           acc.z += v[i][2] * w;
           acc.w += v[i][3] * w;
+          __builtin_amdgcn_raw_buffer_store_b128(empty4, wrs, (ubase + sp * kUnitF4 + c) * 16, 0, kSC1);
         }
-      };
-      floatx4 va[MAXL], vb[MAXL];
-      if (c0 == 0) {
+      }
+    };
+    poll(0, true);
+    if (wave == 0) {
+      float M = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < MAXL; i++) va[i] = pre[i];
-      } else {
-        issue(va, 0);
-      }
-      if (NS <= BS) {
-        consume(va, 0);
-      } else {
-        for (int b0 = 0; b0 < NS; b0 += 2 * BS) {
-          issue(vb, b0 + BS);
-          consume(va, b0);
-          if (b0 + BS >= NS) break;
-          issue(va, b0 + 2 * BS);
-          consume(vb, b0 + BS);
+      for (int j = 0; j < MLC; j++) M = fmaxf(M, ml[j].x);
+      M = wave_max(M);
+      float lt = 0.0f;
+#pragma unroll
+      for (int j = 0; j < MLC; j++) lt += ml[j].y * __builtin_amdgcn_exp2f(ml[j].x - M);
+      lt = wave_sum(lt);
+#pragma unroll
+      for (int j = 0; j < MLC; j++) {
+        const int sp = 64 * j + lane;
+        if (sp < NS) {
+          wts[sp] = __builtin_amdgcn_exp2f(ml[j].x - M) / lt;
+          __builtin_amdgcn_raw_buffer_store_b128(empty4, wrs, (ubase + sp * kUnitF4 + 16) * 16, 0, kSC1);
         }
       }
-      red[(size_t)k * CPT + (c - c0)] = acc;
     }
     __syncthreads();
-    if (act && k == 0) {
-      for (int kk = 1; kk < TPC; kk++) {
-        const float4 v = red[(size_t)kk * CPT + (c - c0)];
-        acc.x += v.x;
-        acc.y += v.y;
-        acc.z += v.z;
-        acc.w += v.w;
+    consume(0);
+    for (int b0 = KG * MAXL; b0 < NS; b0 += KG * MAXL) {
+      poll(b0, false);
+      consume(b0);
+    }
+    // the four split groups of a wave hold the same column in lanes l, l^16, l^32, l^48: two
+    // permlane swaps sum them, then the waves' sums go through LDS
+    {
+      float* a4 = &acc.x;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        float2 t = pair16(a4[e]);
+        a4[e] = t.x + t.y;
+        t = pair32(a4[e]);
+        a4[e] = t.x + t.y;
       }
-      const int rho = (4 * c) / D, d = (4 * c) % D;
-      const int s = rho / p.G, h = kvh * p.G + rho % p.G;
+    }
+    if (lane < 16) red[wave * 16 + c] = acc;
+    __syncthreads();
+    if (tid < 16) {
+#pragma unroll
+      for (int w = 1; w < NW; w++) {
+        const float4 w4 = red[w * 16 + c];
+        acc.x += w4.x;
+        acc.y += w4.y;
+        acc.z += w4.z;
+        acc.w += w4.w;
+      }
+      const int s = rho / p.G, h = kvh * p.G + rho % p.G, d = d0 + 4 * c;
       float r[4] = {acc.x, acc.y, acc.z, acc.w};
       if (p.gate) {
         const float* gr = p.gate + ((size_t)s * p.H + h) * p.gate_stride + d;
@@ -703,64 +767,12 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     }
     __syncthreads();
   }
-  if (tid == 0) __hip_atomic_store(&p.ws_count[kvh], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // ready for the next launch
 }
-
-// ------------------------------------------------------------------------------------------
-// Split merge as a launch of its own, for split lists whose partials are too many for one
-// workgroup to read quickly (n_splits * R * D * 4 bytes per kv head): one wave per (64-dim
-// chunk, row, kv head). Per chunk of up to 64 splits, lane s holds split s's (m, l) and every
-// lane loads its dim of all the chunk's partials at once; the chunk folds into a running
-// log-sum-exp (M, L, acc).
-struct MergeParams {
-  const float* ws_o;   // [KV][n_splits][R][D]
-  const float* ws_ml;  // [KV][n_splits][R][2]
-  int n_splits, R, G, H;
-  const float* gate;
-  int gate_stride;
-  float* out;
-};
-
-template <int D>
-__global__ __launch_bounds__(64) void decode_merge_kernel(MergeParams p) {
-  const int lane = threadIdx.x;
-  const int d = blockIdx.x * 64 + lane, rho = blockIdx.y, kvh = blockIdx.z;
-  const int NS = p.n_splits, R = p.R;
-  const float* o = p.ws_o + (size_t)kvh * NS * R * D + (size_t)rho * D + d;  // + sp * R * D
-  const float* ml = p.ws_ml + (size_t)kvh * NS * R * 2 + (size_t)rho * 2;    // + sp * R * 2
-  float M = -INFINITY, L = 0.0f, acc = 0.0f;
-  for (int s0 = 0; s0 < NS; s0 += 64) {
-    const int nc = min(64, NS - s0);
-    // unconditional loads (indices past the chunk re-read its last split, weight 0)
-    const float2 v = *(const float2*)(ml + (size_t)(s0 + min(lane, nc - 1)) * R * 2);
-    float ov[64];
-#pragma unroll
-    for (int j = 0; j < 64; j++) ov[j] = o[(size_t)(s0 + min(j, nc - 1)) * R * D];
-    const bool ok = lane < nc;
-    const float mi = ok ? v.x : -INFINITY;
-    const float Mn = fmaxf(M, wave_max(mi));
-    const float e = ok ? __builtin_amdgcn_exp2f(mi - Mn) : 0.0f;
-    const float sc = __builtin_amdgcn_exp2f(M - Mn);  // 0 on the first chunk
-    L = L * sc + wave_sum(ok ? v.y * e : 0.0f);
-    acc *= sc;
-#pragma unroll
-    for (int j = 0; j < 64; j++) acc = fmaf(ov[j], __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j)), acc);
-    M = Mn;
-  }
-  const int s = rho / p.G, h = kvh * p.G + rho % p.G;
-  float r = acc / L;
-  if (p.gate) r = r / (1.0f + expf(-p.gate[((size_t)s * p.H + h) * p.gate_stride + d]));
-  p.out[((size_t)s * p.H + h) * D + d] = r;
-}
-
-// partials per kv head above which the merge runs as its own launch (one workgroup reads
-// them at roughly 40-70 GB/s; the extra launch costs about 2 us)
-constexpr size_t kExtMergeBytes = 96 * 1024;
 
 static int nset_for(int R) { return (R + 15) / 16; }
 
 // dynamic LDS of the tile loop and wave combine (DecodeSmem::total for the launch's template
-// arguments); the in-launch split merge needs less (at most 96 KB of partials per kv head)
+// arguments); the split merge needs less (weights and 16 float4 per split group)
 static size_t decode_lds_bytes(int D, int dtype, int R) {
   const int nset = nset_for(R);
   const int NW = (D == 128 && nset == 1) ? 8 : 4;
@@ -794,18 +806,25 @@ static Split plan_split(const LayerView& L, int S, int pos_base, int num_cus, in
   // one workgroup per CU: tiles_per_split = ceil(tiles * KV / CUs), at least one tile per wave
   int tps = (s.n_tiles * L.kv_heads + cus - 1) / cus;
   tps = tps < nw ? nw : tps;
+  const int tps_min = (s.n_tiles + kMaxSplits - 1) / kMaxSplits;
+  tps = tps < tps_min ? tps_min : tps;
   s.tps = tps;
   s.n_splits = (s.n_tiles + tps - 1) / tps;
   return s;
 }
 
+uint32_t decode_workspace_empty() { return kPartialEmpty; }
+
 size_t decode_workspace_floats(const LayerView& L, int S, int H, int num_cus, size_t* counters) {
   // upper bound over every pos_base: tiles_per_split >= 4 waves, so at most cap/32/4 splits
+  // (and kMaxSplits); one 17-float4 slot per (kv head, unit, split). The caller fills it with
+  // kPartialEmpty once (decode_workspace_fill) and every launch leaves it that way.
   (void)num_cus;
   const int R = (H / L.kv_heads) * S;
-  const int ns_max = (L.cap / 32 + 3) / 4;
+  int ns_max = (L.cap / 32 + 3) / 4;
+  ns_max = ns_max < kMaxSplits ? ns_max : kMaxSplits;
   *counters = (size_t)L.kv_heads;
-  return (size_t)L.kv_heads * ns_max * R * ((size_t)L.D + 2);
+  return (size_t)L.kv_heads * R * (L.D / 64) * ns_max * kUnitF4 * 4;
 }
 
 template <int D, int DT, bool ROLL, int NSET>
@@ -830,21 +849,17 @@ static hipError_t launch_cfg(const LayerView& L, const AttnArgs& a, hipStream_t 
   p.n_tiles = sp.n_tiles;
   p.tiles_per_split = sp.tps;
   p.n_splits = sp.n_splits;
-  const size_t need = (size_t)L.kv_heads * sp.n_splits * p.R * ((size_t)D + 2);
-  if (sp.n_splits > 1 && (a.ws_o == nullptr || need > a.ws_floats)) return hipErrorInvalidValue;
-  p.ws_o = a.ws_o;
-  p.ws_ml = a.ws_o ? a.ws_o + (size_t)L.kv_heads * sp.n_splits * p.R * D : nullptr;
-  p.ws_count = a.ws_count;
-  p.merge_ext = sp.n_splits > 1 && (size_t)sp.n_splits * p.R * D * 4 > kExtMergeBytes;
+  const int units = p.R * (D / 64);  // merge units: one row x 64 dims
+  const size_t need = (size_t)L.kv_heads * units * sp.n_splits * kUnitF4 * 4;
+  if (sp.n_splits > 1 && (a.ws_o == nullptr || need > a.ws_floats || sp.n_splits > kMaxSplits)) return hipErrorInvalidValue;
+  p.ws = (float4*)a.ws_o;
+  p.n_mergers = units < sp.n_splits ? units : sp.n_splits;
   const int NP = (p.R + 3) / 4;
   size_t smem = SM::total(NP, p.R);
   if (smem != decode_lds_bytes(D, DT, p.R)) return hipErrorInvalidValue;  // the two plans agree
-  if (sp.n_splits > 1 && !p.merge_ext) {
-    // the in-launch merge reuses the space: weights + l [NS][R] and float4 partial sums
-    const size_t C4 = (size_t)p.R * D / 4;
-    const size_t tpc = (size_t)64 * NW >= C4 ? (size_t)64 * NW / C4 : 1;
-    const size_t cpt = (size_t)64 * NW / tpc;
-    const size_t merge = (size_t)3 * sp.n_splits * p.R * 4 + tpc * cpt * 16;
+  if (sp.n_splits > 1) {
+    // the merge reuses the space: weights [NS] (16-byte aligned) and [waves][16] float4
+    const size_t merge = (((size_t)sp.n_splits * 4 + 15) & ~(size_t)15) + (size_t)NW * 16 * 16;
     smem = smem > merge ? smem : merge;
   }
   if (smem > kDecodeLdsMax) return hipErrorInvalidValue;
@@ -858,19 +873,6 @@ static hipError_t launch_cfg(const LayerView& L, const AttnArgs& a, hipStream_t 
     }
   }
   hipLaunchKernelGGL((decode_kernel<D, DT, ROLL, NSET, NW>), dim3(sp.n_splits * L.kv_heads), dim3(64 * NW), smem, st, p);
-  if (p.merge_ext) {
-    MergeParams m;
-    m.ws_o = p.ws_o;
-    m.ws_ml = p.ws_ml;
-    m.n_splits = p.n_splits;
-    m.R = p.R;
-    m.G = p.G;
-    m.H = p.H;
-    m.gate = p.gate;
-    m.gate_stride = p.gate_stride;
-    m.out = p.out;
-    hipLaunchKernelGGL((decode_merge_kernel<D>), dim3(D / 64, p.R, L.kv_heads), dim3(64), 0, st, m);
-  }
   return hipGetLastError();
 }
 
