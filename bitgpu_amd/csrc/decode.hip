@@ -212,9 +212,12 @@ __device__ __forceinline__ void load_tile(TileRegs<D, DT, QUARTER>& T, int j0, i
   load_tile_v<D, DT, QUARTER>(T, j0, g, n, vbase);
 }
 
-template <int D, int DT, bool ROLL, int NSET, int NW>
+// NPT > 0: the launch has exactly NPT passes of 4 query rows (compiled straight-line); 0: up to
+// the set's RS / 4 passes, counted at run time
+template <int D, int DT, bool ROLL, int NSET, int NW, int NPT>
 __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
   using SM = DecodeSmem<D, DT, ROLL, NSET, NW>;
+  constexpr int NPK = NPT > 0 ? NPT : SM::NPMAX;  // passes compiled
   constexpr bool QUARTER = SM::QUARTER;
   constexpr int NT = SM::NT;
   constexpr int NBV = SM::NBV;
@@ -235,7 +238,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
   const int n = lane & 15;
   const int kvh = blockIdx.x % p.L.kv_heads;
   const int split = blockIdx.x / p.L.kv_heads;
-  const int NP = (p.R + 3) >> 2;
+  const int NP = NPT > 0 ? NPT : (p.R + 3) >> 2;
 
   uint4* qs = (uint4*)smem;                                           // [NP][NT][2][64]
   unsigned char* pbase = smem + SM::q_bytes(NP);
@@ -259,7 +262,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
   TileRegs<D, DT, QUARTER> A, B;
   const int tile0 = t_begin + wave;
   {
-    constexpr int QMAX = (SM::NPMAX * NT * 64 + NTHR - 1) / NTHR;  // operand slots per thread
+    constexpr int QMAX = (NPK * NT * 64 + NTHR - 1) / NTHR;  // operand slots per thread
     const int NQ = NP * NT * 64;
     float qv[QMAX][8];
     bool use[QMAX];
@@ -308,9 +311,9 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
   }
   __syncthreads();
 
-  float m[SM::NPMAX], lsum[SM::NPMAX];
+  float m[NPK], lsum[NPK];
 #pragma unroll
-  for (int i = 0; i < SM::NPMAX; i++) { m[i] = -1e30f; lsum[i] = 0.0f; }
+  for (int i = 0; i < NPK; i++) { m[i] = -1e30f; lsum[i] = 0.0f; }
   floatx4 o[NSET][D / 16];
 #pragma unroll
   for (int s = 0; s < NSET; s++)
@@ -386,7 +389,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
 
     // ---------------- QK + online softmax, one pass per 4 query rows ----------------
 #pragma unroll
-    for (int pass = 0; pass < SM::NPMAX; pass++) {
+    for (int pass = 0; pass < NPK; pass++) {
       if (pass >= NP) break;
       float sc[2];
 #pragma unroll
@@ -561,7 +564,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
   // (rows padded by 4 floats to spread the banks); the sum over the waves is plain adds.
   __shared__ float s_mw[NW][RS];
 #pragma unroll
-  for (int pass = 0; pass < SM::NPMAX; pass++) {
+  for (int pass = 0; pass < NPK; pass++) {
     if (pass >= NP) break;
     const int rho = 4 * pass + g;
     if (n == 0 && rho < p.R) s_mw[wave][rho] = m[pass];
@@ -577,7 +580,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     return M;
   };
 #pragma unroll
-  for (int pass = 0; pass < SM::NPMAX; pass++) {
+  for (int pass = 0; pass < NPK; pass++) {
     if (pass >= NP) break;
     const float lt = group16_sum(lsum[pass]);
     const int rho = 4 * pass + g;
@@ -827,7 +830,7 @@ size_t decode_workspace_floats(const LayerView& L, int S, int H, int num_cus, si
   return (size_t)L.kv_heads * R * (L.D / 64) * ns_max * kUnitF4 * 4;
 }
 
-template <int D, int DT, bool ROLL, int NSET>
+template <int D, int DT, bool ROLL, int NSET, int NPT>
 static hipError_t launch_cfg(const LayerView& L, const AttnArgs& a, hipStream_t st) {
   constexpr int NW = (D == 128 && NSET == 1) ? 8 : 4;
   using SM = DecodeSmem<D, DT, ROLL, NSET, NW>;
@@ -866,22 +869,27 @@ static hipError_t launch_cfg(const LayerView& L, const AttnArgs& a, hipStream_t 
   if (smem > 64 * 1024) {
     static size_t attr_bytes = 0;
     if (smem > attr_bytes) {
-      hipError_t e = hipFuncSetAttribute((const void*)decode_kernel<D, DT, ROLL, NSET, NW>,
+      hipError_t e = hipFuncSetAttribute((const void*)decode_kernel<D, DT, ROLL, NSET, NW, NPT>,
                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
       if (e != hipSuccess) return e;
       attr_bytes = smem;
     }
   }
-  hipLaunchKernelGGL((decode_kernel<D, DT, ROLL, NSET, NW>), dim3(sp.n_splits * L.kv_heads), dim3(64 * NW), smem, st, p);
+  hipLaunchKernelGGL((decode_kernel<D, DT, ROLL, NSET, NW, NPT>), dim3(sp.n_splits * L.kv_heads), dim3(64 * NW), smem, st, p);
   return hipGetLastError();
 }
 
 template <int D, int DT, bool ROLL>
 static hipError_t launch_nset(const LayerView& L, const AttnArgs& a, int nset, hipStream_t st) {
+  const int np = ((a.H / L.kv_heads) * a.S + 3) / 4;  // passes of 4 query rows
   switch (nset) {
-    case 1: return launch_cfg<D, DT, ROLL, 1>(L, a, st);
-    case 2: return launch_cfg<D, DT, ROLL, 2>(L, a, st);
-    default: return launch_cfg<D, DT, ROLL, 3>(L, a, st);
+    case 1:
+      // decode shapes (G = 4 or 6 rows) get straight-line passes
+      if (np == 1) return launch_cfg<D, DT, ROLL, 1, 1>(L, a, st);
+      if (np == 2) return launch_cfg<D, DT, ROLL, 1, 2>(L, a, st);
+      return launch_cfg<D, DT, ROLL, 1, 0>(L, a, st);
+    case 2: return launch_cfg<D, DT, ROLL, 2, 0>(L, a, st);
+    default: return launch_cfg<D, DT, ROLL, 3, 0>(L, a, st);
   }
 }
 
