@@ -458,15 +458,32 @@ __global__ __launch_bounds__(256 * TEAMS) void prefill_kernel(PrefillParams p) {
       for (int u = 0; u < NA; u++)
 #pragma unroll
         for (int e = 0; e < 16; e++) sacc[u][e] = 0.0f;
+      // K operands read two dim chunks ahead of the MFMAs that use them, so each chunk's MFMAs
+      // cover later chunks' LDS latency
+      {
+        PH8 ka[NC][NSUB];
 #pragma unroll
-      for (int c = 0; c < NC; c++)
+        for (int c = 0; c < NC; c++)
 #pragma unroll
-        for (int u = 0; u < NSUB; u++) {
-          PH8 a;
-          a.u = ldv(kc + k_chunk_pos<D>(u * 32 + n, 2 * c + g2) * 8);
-          const int acc = NSUB == 1 ? (c & 1) : u;
-          sacc[acc] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a.h, qf[c], sacc[acc], 0, 0, 0);
+          for (int u = 0; u < NSUB; u++) ka[c][u].u = ldv(kc + k_chunk_pos<D>(u * 32 + n, 2 * c + g2) * 8);
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+#pragma unroll
+          for (int u = 0; u < NSUB; u++) {
+            const int acc = NSUB == 1 ? (c & 1) : u;
+            sacc[acc] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[c][u].h, qf[c], sacc[acc], 0, 0, 0);
+          }
         }
+        // schedule: the reads of two dim chunks first, then each chunk's MFMAs followed by the
+        // reads two chunks ahead (left alone, the scheduler waits for every read pair in turn)
+        __builtin_amdgcn_sched_group_barrier(0x100, 2 * NSUB, 0);
+#pragma unroll
+        for (int c = 0; c < NC - 1; c++) {
+          __builtin_amdgcn_sched_group_barrier(0x008, NSUB, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, NSUB, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, NSUB, 0);
+      }
       if constexpr (NSUB == 1) sacc[0] += sacc[1];
       // mask + online softmax (row = this lane's n)
       float x[NSUB][16];
@@ -507,6 +524,14 @@ __global__ __launch_bounds__(256 * TEAMS) void prefill_kernel(PrefillParams p) {
       }
       // P = exp2(S - m) as the f16 B operand of P^T; O^T += V^T P^T
       const half2p ones = {(_Float16)1.0f, (_Float16)1.0f};
+      // V^T operands of 32-key group (u, t) for every output dim chunk; read ahead of the MFMAs
+      // that use them (see the schedule below)
+      PH8 va[2 * NSUB][ND];
+#pragma unroll
+      for (int ut = 0; ut < 2 * NSUB; ut++)
+#pragma unroll
+        for (int dc = 0; dc < ND; dc++)
+          va[ut][dc].u = ldv(vc + ((size_t)((ut >> 1) * 4 + 2 * (ut & 1) + g2) * D + 32 * dc + n) * 8);
 #pragma unroll
       for (int u = 0; u < NSUB; u++)
 #pragma unroll
@@ -519,14 +544,19 @@ __global__ __launch_bounds__(256 * TEAMS) void prefill_kernel(PrefillParams p) {
           }
 #pragma unroll
           for (int i = 0; i < 4; i++) lsum = __builtin_amdgcn_fdot2(pb.p[i], ones, lsum, false);
-          const int pnl = 2 * t + g2;
 #pragma unroll
-          for (int dc = 0; dc < ND; dc++) {
-            PH8 a;
-            a.u = ldv(vc + ((size_t)(u * 4 + pnl) * D + 32 * dc + n) * 8);
-            o[dc] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a.h, pb.h, o[dc], 0, 0, 0);
-          }
+          for (int dc = 0; dc < ND; dc++)
+            o[dc] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[2 * u + t][dc].h, pb.h, o[dc], 0, 0, 0);
         }
+      // schedule: the V^T reads of the first key group, then each group's MFMAs followed by the
+      // next group's reads
+      __builtin_amdgcn_sched_group_barrier(0x100, ND, 1);
+#pragma unroll
+      for (int ut = 0; ut < 2 * NSUB - 1; ut++) {
+        __builtin_amdgcn_sched_group_barrier(0x100, ND, 1);
+        __builtin_amdgcn_sched_group_barrier(0x008, ND, 1);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, ND, 1);
 
       if constexpr (DMA) {
         __builtin_amdgcn_s_waitcnt(0xf70);  // vmcnt(0): this wave's copies of step s+1 landed
