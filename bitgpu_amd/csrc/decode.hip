@@ -612,19 +612,39 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
   const int units = p.R * UPR;
   const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(p.ws + (size_t)kvh * units * NS * kUnitF4), (short)0, 0x7fffffff, 0x00020000);
-  for (int c = tid; c < C4; c += NTHR) {
+  // Each float4 column of the R x D partial is summed by 4 adjacent lanes (NW/4 waves each,
+  // all LDS reads independent) whose sums meet by DPP; the first lane of the four stores it.
+  constexpr int WPT = NW / 4;
+  const int q4 = tid & 3;
+  for (int c = tid >> 2; c < C4; c += NTHR / 4) {
     const int rho = c / (D / 4), d = 4 * (c % (D / 4));
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    float lt = 0.0f;
+    float4 v[WPT];
+    float lv[WPT], mv[WPT];
 #pragma unroll
-    for (int w = 0; w < NW; w++) {
-      const float4 v = *(const float4*)(ow + ((size_t)w * p.R + rho) * DP + d);
-      acc.x += v.x;
-      acc.y += v.y;
-      acc.z += v.z;
-      acc.w += v.w;
-      lt += lw[w * p.R + rho];
+    for (int j = 0; j < WPT; j++) {
+      const int w = q4 * WPT + j;
+      v[j] = *(const float4*)(ow + ((size_t)w * p.R + rho) * DP + d);
+      lv[j] = lw[w * p.R + rho];
+      mv[j] = s_mw[w][rho];
     }
+    float4 acc = v[0];
+    float lt = lv[0], mx = mv[0];
+#pragma unroll
+    for (int j = 1; j < WPT; j++) {
+      acc.x += v[j].x;
+      acc.y += v[j].y;
+      acc.z += v[j].z;
+      acc.w += v[j].w;
+      lt += lv[j];
+      mx = fmaxf(mx, mv[j]);
+    }
+    acc.x = group_sum<4>(acc.x);
+    acc.y = group_sum<4>(acc.y);
+    acc.z = group_sum<4>(acc.z);
+    acc.w = group_sum<4>(acc.w);
+    lt = group_sum<4>(lt);
+    mx = group_max<4>(mx);
+    if (q4 != 0) continue;
     if (single) {
       const int s = rho / p.G, h = kvh * p.G + rho % p.G;
       float r[4] = {acc.x / lt, acc.y / lt, acc.z / lt, acc.w / lt};
@@ -638,7 +658,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
       const int slot = ((rho * UPR + d / 64) * NS + split) * kUnitF4;
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4v, acc), wrs, (slot + (d % 64) / 4) * 16, 0, kSC1);
       if (d % 64 == 0) {
-        const float4 ml = make_float4(row_max(rho), lt, 0.0f, 0.0f);
+        const float4 ml = make_float4(mx, lt, 0.0f, 0.0f);
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4v, ml), wrs, (slot + 16) * 16, 0, kSC1);
       }
     }
