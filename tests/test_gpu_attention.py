@@ -139,17 +139,41 @@ def test_decode_gate_hybrid_shape(dev):
     _check("q8", out, exp)
 
 
-# Split merges. On 256 CUs the split count is about 256 / KV; the merge runs inside the decode
-# launch (last workgroup of a kv head) up to 96 KB of partials per kv head, above that as a
-# launch of its own. Shapes: (24,4,256) L=4097 -> 33 splits x 6 rows x 1 KB (own launch);
-# (16,2,128) L=32768 -> 128 splits, two 64-split chunks (own launch); (2,2,128) L=32768 -> 128
-# splits of one row (in the launch, weights through LDS); (32,8,128) S=12 -> 48 rows (own launch).
+# Split merges. On 256 CUs the split count is about 256 / KV. Every split writes its partial into
+# the cache's workspace (slots hold an "empty" marker between launches) and the first splits of a
+# kv head merge one (row, 64-dim) unit each. Shapes: (24,4,256) L=4097 -> 52 splits, 24 units;
+# (16,2,128) L=32768 -> 128 splits (one poll batch of 128); (2,2,128) -> 128 splits of one row;
+# (4,1,256) L=32768 -> 256 splits, polled in four batches of 64; (32,8,128) S=12 -> 48 rows.
 @pytest.mark.parametrize("dtype", ["f16", "q8"])
 @pytest.mark.parametrize("H,KV,D,L,S,gate", [(24, 4, 256, 4097, 1, True), (16, 2, 128, 32768, 1, False),
-                                             (2, 2, 128, 32768, 1, False), (32, 8, 128, 4108, 12, False)])
+                                             (2, 2, 128, 32768, 1, False), (4, 1, 256, 32768, 1, False),
+                                             (32, 8, 128, 4108, 12, False)])
 def test_decode_merge_paths(dev, dtype, H, KV, D, L, S, gate):
     out, exp = _raw_case(dtype, H, KV, D, L, S, seed=L + H, gate=gate)
     _check(dtype, out, exp)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "q8"])
+def test_decode_workspace_reuse(dev, dtype):
+    """Consecutive launches with different split counts, row counts and layers share one
+    workspace: each launch must leave every slot empty for the next (a stale partial read as
+    fresh would be merged into the wrong output)."""
+    H, KV, D, L = 32, 8, 128, 8192
+    rng = np.random.default_rng(77)
+    c = E.KvCache(2, KV, D, dtype, max_seq_len=L, capacity=L)
+    kv = []
+    for li in (0, 1):
+        k = rng.standard_normal((L, KV, D)).astype(np.float32)
+        v = rng.standard_normal((L, KV, D)).astype(np.float32)
+        fill_cache_raw(c, li, k, v)
+        kv.append(cached_values(c, li, 0, L))
+    # (layer, query rows, positions attended): 256 / 16 / 128 / 1 splits, 4 / 20 / 48 rows
+    for li, S, upto in [(0, 1, L), (1, 1, 300), (0, 5, 4000), (1, 12, L), (0, 1, L), (1, 1, 33), (0, 1, 4096)]:
+        q = rng.standard_normal((S, H, D)).astype(np.float32)
+        out = run_attention(c, li, q, upto - S)
+        exp = ref.attention(q, kv[li][0], kv[li][1], upto - S)
+        _check(dtype, out, exp)
+    c.close()
 
 
 # ------------------------------------------------------------------ f32 kernel
