@@ -33,6 +33,9 @@ struct bg_kv_cache {
   size_t ws_floats = 0;
   unsigned* ws_count = nullptr;
   size_t ws_counters = 0;
+  // f16 copy of one q8 layer's attended slots for long prefills (K then V, cap_copy slots each)
+  void* pf16 = nullptr;
+  int pf16_cap = 0;
   int num_cus = 256;
 };
 
@@ -299,6 +302,7 @@ int32_t bg_kv_destroy(bg_kv_cache* c) {
   free_layers(c->k, c->v, c->ks, c->vs);
   if (c->ws) (void)hipFree(c->ws);
   if (c->ws_count) (void)hipFree(c->ws_count);
+  if (c->pf16) (void)hipFree(c->pf16);
   delete c;
   return BG_OK;
 }
@@ -470,8 +474,32 @@ static int32_t ensure_workspace(bg_kv_cache* c, int S, int H) {
   return BG_OK;
 }
 
+// the f16 prefill copy holds one layer at the cache's physical capacity (zero-filled, so slots
+// past the dequantized range read as finite zeros)
+static int32_t ensure_prefill_copy(bg_kv_cache* c) {
+  if (c->pf16 && c->pf16_cap == c->cap) return BG_OK;
+  if (c->pf16) (void)hipFree(c->pf16);
+  c->pf16 = nullptr;
+  c->pf16_cap = 0;
+  const size_t bytes = (size_t)2 * c->kv_heads * c->cap * c->D * sizeof(uint16_t);
+  hipError_t e = hipMalloc(&c->pf16, bytes);
+  if (e == hipSuccess) e = hipMemset(c->pf16, 0, bytes);
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e != hipSuccess) {
+    if (c->pf16) (void)hipFree(c->pf16);
+    c->pf16 = nullptr;
+    return hip_fail(e, "prefill f16 copy allocation");
+  }
+  c->pf16_cap = c->cap;
+  return BG_OK;
+}
+
 int32_t bg_attention_reserve(bg_kv_cache* c, int32_t S, int32_t H) {
   if (!c || S < 1 || H < 1 || H % c->kv_heads) return fail(BG_E_INVALID, "bg_attention_reserve: bad arguments");
+  if (bg::prefill_wants_f16_copy(view(c, 0), S, H) && !bg::decode_supported(view(c, 0), S, H)) {
+    int32_t rc = ensure_prefill_copy(c);
+    if (rc != BG_OK) return rc;
+  }
   if (!bg::decode_supported(view(c, 0), S, H) && !bg::f32_split_supported(view(c, 0), S, H)) return BG_OK;
   return ensure_workspace(c, S, H);
 }
@@ -527,7 +555,23 @@ int32_t bg_attention(bg_kv_cache* c, int32_t layer, const float* q, int32_t S, i
     a.ws_floats = c->ws_floats;
     e = bg::launch_attention_decode(L, a, st);
   } else if (bg::prefill_supported(L, S, H)) {
-    e = bg::launch_attention_prefill(L, a, st);
+    if (bg::prefill_wants_f16_copy(L, S, H)) {
+      // dequantize the attended slots once, then run the f16 path on the copy
+      int32_t rc = ensure_prefill_copy(c);
+      if (rc != BG_OK) return rc;
+      int n = (pos_base + S + 63) & ~63;
+      n = n < c->cap ? n : c->cap;
+      LayerView F = L;
+      F.k = c->pf16;
+      F.v = (uint16_t*)c->pf16 + (size_t)c->kv_heads * c->cap * c->D;
+      F.ks = nullptr;
+      F.vs = nullptr;
+      F.dtype = bg::KV_F16;
+      e = bg::launch_kv_dequant_f16(L, n, F.k, F.v, st);
+      if (e == hipSuccess) e = bg::launch_attention_prefill(F, a, st);
+    } else {
+      e = bg::launch_attention_prefill(L, a, st);
+    }
   } else {
     return fail(BG_E_UNSUPPORTED, "bg_attention: no kernel for S %d, heads %d", S, H);
   }

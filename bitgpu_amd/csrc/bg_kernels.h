@@ -33,6 +33,9 @@ hipError_t launch_kv_write(const LayerView& L, int which, const float* src, int 
                            hipStream_t st);
 hipError_t launch_kv_export(const LayerView& L, int region, int base, int count, void* dst, hipStream_t st);
 hipError_t launch_kv_import(const LayerView& L, int region, int base, int count, const void* src, hipStream_t st);
+// q8 layer -> f16 copy of slots [0, n_slots) (n_slots a multiple of 32) laid out like an f16
+// cache of the same capacity, with the q8 prefill staging's exact values
+hipError_t launch_kv_dequant_f16(const LayerView& L, int n_slots, void* kdst, void* vdst, hipStream_t st);
 
 // norm_rope.hip
 struct PrologueArgs {
@@ -71,5 +74,8 @@ size_t decode_workspace_floats(const LayerView& L, int S, int H, int num_cus, si
 uint32_t decode_workspace_empty();
 bool decode_supported(const LayerView& L, int S, int H);
 bool prefill_supported(const LayerView& L, int S, int H);
+// a q8 prefill of S rows that stages each K/V tile for enough query blocks to run faster on an
+// f16 copy of the attended slots
+bool prefill_wants_f16_copy(const LayerView& L, int S, int H);
 
 }  // namespace bg

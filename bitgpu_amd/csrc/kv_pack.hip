@@ -92,4 +92,70 @@ hipError_t launch_kv_import(const LayerView& L, int region, int base, int count,
   return hipGetLastError();
 }
 
+// ---- q8 -> f16 copy of the attended slots, for a long prefill ---------------------------------
+// A q8 prefill stages (dequantizes) every K/V tile once per query block that attends it. For a
+// long prompt the attended slots are dequantized once here into an f16 copy laid out like an f16
+// cache (K row-major, V in 32-slot transposed tiles), and the prefill runs its direct-to-LDS f16
+// path on that copy. The values are exactly the ones the q8 staging produces: the code, biased
+// to u = code + 128, times s = scale * (1/127) in one f32 fma (u * s - 128 * s), then RNE to f16.
+__device__ inline _Float16 q8_staged_f16(uint32_t u, float s) { return (_Float16)fmaf((float)u, s, -128.0f * s); }
+
+template <int D>
+__global__ __launch_bounds__(256) void kv_dequant_kernel(LayerView L, int n_slots, __half* __restrict__ kdst,
+                                                         __half* __restrict__ vdst) {
+  constexpr int NB = D / kBlock;
+  const size_t per_head = (size_t)n_slots * D / 16;  // 16-value chunks of K (and of V) per kv head
+  const size_t total = per_head * L.kv_heads;
+  for (size_t c = (size_t)blockIdx.x * blockDim.x + threadIdx.x; c < 2 * total; c += (size_t)gridDim.x * blockDim.x) {
+    const bool isv = c >= total;
+    const size_t cc = isv ? c - total : c;
+    const int kvh = (int)(cc / per_head);
+    const size_t e0 = (cc % per_head) * 16;  // element offset inside the kv head's region
+    const size_t base = (size_t)kvh * L.cap * D;
+    const uint4 w = *(const uint4*)((const int8_t*)(isv ? L.v : L.k) + base + e0);
+    const uint32_t ww[4] = {w.x ^ 0x80808080u, w.y ^ 0x80808080u, w.z ^ 0x80808080u, w.w ^ 0x80808080u};
+    _Float16 o[16];
+    if (!isv) {
+      const int slot = (int)(e0 / D), d0 = (int)(e0 % D);
+      const float s = L.ks[((size_t)kvh * L.cap + slot) * NB + d0 / kBlock] * (1.0f / 127.0f);
+#pragma unroll
+      for (int i = 0; i < 16; i++) o[i] = q8_staged_f16((ww[i >> 2] >> (8 * (i & 3))) & 0xffu, s);
+      uint4* dst = (uint4*)(kdst + base + e0);
+      dst[0] = *(const uint4*)&o[0];
+      dst[1] = *(const uint4*)&o[8];
+    } else {
+      // 16 bytes of a V tile = 2 dims x the 8 slots of one panel
+      const int t = (int)(e0 / ((size_t)kTile * D));
+      const int wi = (int)(e0 % ((size_t)kTile * D));
+      const int panel = wi / (8 * D), d0 = (wi % (8 * D)) / 8;
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        const int d = d0 + h;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          const int slot = t * kTile + tile_slot(panel, e);
+          const float s = L.vs[((size_t)kvh * L.cap + slot) * NB + d / kBlock] * (1.0f / 127.0f);
+          const int i = 8 * h + e;
+          o[i] = q8_staged_f16((ww[i >> 2] >> (8 * (i & 3))) & 0xffu, s);
+        }
+      }
+      uint4* dst = (uint4*)(vdst + base + e0);
+      dst[0] = *(const uint4*)&o[0];
+      dst[1] = *(const uint4*)&o[8];
+    }
+  }
+}
+
+hipError_t launch_kv_dequant_f16(const LayerView& L, int n_slots, void* kdst, void* vdst, hipStream_t st) {
+  if (L.dtype != KV_Q8 || n_slots <= 0 || n_slots % kTile || n_slots > L.cap) return hipErrorInvalidValue;
+  const size_t chunks = 2 * (size_t)n_slots * L.D / 16 * L.kv_heads;
+  const int grid = (int)((chunks + 255) / 256 < 4096 ? (chunks + 255) / 256 : 4096);
+  switch (L.D) {
+    case 64: hipLaunchKernelGGL((kv_dequant_kernel<64>), dim3(grid), dim3(256), 0, st, L, n_slots, (__half*)kdst, (__half*)vdst); break;
+    case 128: hipLaunchKernelGGL((kv_dequant_kernel<128>), dim3(grid), dim3(256), 0, st, L, n_slots, (__half*)kdst, (__half*)vdst); break;
+    default: hipLaunchKernelGGL((kv_dequant_kernel<256>), dim3(grid), dim3(256), 0, st, L, n_slots, (__half*)kdst, (__half*)vdst); break;
+  }
+  return hipGetLastError();
+}
+
 }  // namespace bg

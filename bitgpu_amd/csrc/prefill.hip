@@ -687,6 +687,15 @@ bool prefill_supported(const LayerView& L, int S, int H) {
   return G >= 1 && G <= 128 && S >= 1;
 }
 
+bool prefill_wants_f16_copy(const LayerView& L, int S, int H) {
+  // each K/V tile is staged once per query block (128 rows of (query, head) pairs); from four
+  // blocks on, one dequantizing pass plus the f16 direct-to-LDS staging costs less
+  if (L.dtype != KV_Q8 || L.ring.roll) return false;
+  const int G = H / L.kv_heads;
+  const int QB = 128 / G;
+  return (S + QB - 1) / QB >= 4;
+}
+
 // two teams where the registers allow two waves per SIMD (D=128); D=256 keeps its O and Q^T in
 // one wave per SIMD's 512 registers
 template <int D, int DT, bool ROLL>
