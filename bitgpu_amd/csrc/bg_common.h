@@ -74,6 +74,18 @@ __device__ inline int q8_code(float v, float s) {
 }
 __device__ inline float q8_scale_of(float absmax) { return fmaxf(absmax, 1e-30f); }
 
+// q8 -> f16 MFMA operand, the one definition shared by the prefill staging and the prefill's f16
+// copy: u = code + 128 (the biased byte), s = scale * (1/127) in f32, the f32 fma u*s - 128*s
+// (one rounding of code * s), then RNE to f16. The f32 value is pinned so the compiler cannot
+// fuse the fma and the conversion into a mixed-precision fma (one rounding instead of two),
+// which it does for some call sites and not others.
+__device__ inline float q8_stage_f32(uint32_t u, float s) {
+  float a = fmaf((float)u, s, -128.0f * s);
+  asm("" : "+v"(a));
+  return a;
+}
+__device__ inline _Float16 q8_stage_f16(uint32_t u, float s) { return (_Float16)q8_stage_f32(u, s); }
+
 // ---- cross-lane exchange and reductions, all in the VALU (no LDS round trip) ----
 // Inside a 16-lane row: DPP quad_perm [1,0,3,2] and [2,3,0,1] pair lanes i^1 and i^2; once a
 // quad holds one value, row_half_mirror (lane 7-i of each 8) and then row_mirror (lane 15-i)

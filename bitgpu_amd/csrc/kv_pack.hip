@@ -97,8 +97,8 @@ hipError_t launch_kv_import(const LayerView& L, int region, int base, int count,
 // long prompt the attended slots are dequantized once here into an f16 copy laid out like an f16
 // cache (K row-major, V in 32-slot transposed tiles), and the prefill runs its direct-to-LDS f16
 // path on that copy. The values are exactly the ones the q8 staging produces: the code, biased
-// to u = code + 128, times s = scale * (1/127) in one f32 fma (u * s - 128 * s), then RNE to f16.
-__device__ inline _Float16 q8_staged_f16(uint32_t u, float s) { return (_Float16)fmaf((float)u, s, -128.0f * s); }
+// to u = code + 128, times s = scale * (1/127) in one f32 fma (u * s - 128 * s), then RNE to f16
+// (q8_stage_f16).
 
 template <int D>
 __global__ __launch_bounds__(256) void kv_dequant_kernel(LayerView L, int n_slots, __half* __restrict__ kdst,
@@ -119,7 +119,7 @@ __global__ __launch_bounds__(256) void kv_dequant_kernel(LayerView L, int n_slot
       const int slot = (int)(e0 / D), d0 = (int)(e0 % D);
       const float s = L.ks[((size_t)kvh * L.cap + slot) * NB + d0 / kBlock] * (1.0f / 127.0f);
 #pragma unroll
-      for (int i = 0; i < 16; i++) o[i] = q8_staged_f16((ww[i >> 2] >> (8 * (i & 3))) & 0xffu, s);
+      for (int i = 0; i < 16; i++) o[i] = q8_stage_f16((ww[i >> 2] >> (8 * (i & 3))) & 0xffu, s);
       uint4* dst = (uint4*)(kdst + base + e0);
       dst[0] = *(const uint4*)&o[0];
       dst[1] = *(const uint4*)&o[8];
@@ -136,7 +136,7 @@ __global__ __launch_bounds__(256) void kv_dequant_kernel(LayerView L, int n_slot
           const int slot = t * kTile + tile_slot(panel, e);
           const float s = L.vs[((size_t)kvh * L.cap + slot) * NB + d / kBlock] * (1.0f / 127.0f);
           const int i = 8 * h + e;
-          o[i] = q8_staged_f16((ww[i >> 2] >> (8 * (i & 3))) & 0xffu, s);
+          o[i] = q8_stage_f16((ww[i >> 2] >> (8 * (i & 3))) & 0xffu, s);
         }
       }
       uint4* dst = (uint4*)(vdst + base + e0);

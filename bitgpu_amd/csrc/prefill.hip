@@ -205,8 +205,8 @@ struct Stager {
         const uint32_t ua = wa[i] ^ 0x80808080u, ub = wb[i] ^ 0x80808080u;  // biased: u = c + 128
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-          a[4 * i + e] = fmaf((float)((ua >> (8 * e)) & 0xffu), sa, -128.0f * sa);  // = c * sa, one rounding
-          b[4 * i + e] = fmaf((float)((ub >> (8 * e)) & 0xffu), sb, -128.0f * sb);
+          a[4 * i + e] = q8_stage_f32((ua >> (8 * e)) & 0xffu, sa);  // = c * sa, one f32 rounding
+          b[4 * i + e] = q8_stage_f32((ub >> (8 * e)) & 0xffu, sb);
         }
       }
     } else {
@@ -265,19 +265,16 @@ struct Stager {
     }
     if constexpr (DT == KV_Q8) {
       const uint32_t w[8] = {R.v[0][0], R.v[0][1], R.v[0][2], R.v[0][3], R.v[1][0], R.v[1][1], R.v[1][2], R.v[1][3]};
-      float sv[8], nb[8];
+      float sv[8];
 #pragma unroll
-      for (int e = 0; e < 8; e++) {
-        sv[e] = R.vsc[e] * (1.0f / 127.0f);
-        nb[e] = -128.0f * sv[e];
-      }
+      for (int e = 0; e < 8; e++) sv[e] = R.vsc[e] * (1.0f / 127.0f);
 #pragma unroll
       for (int i = 0; i < 4; i++) {  // chunk i: dim 4*vdg + i, 8 slots
         PH8 o;
 #pragma unroll
         for (int e = 0; e < 8; e++) {
           const uint32_t u = w[2 * i + (e >> 2)] ^ 0x80808080u;
-          o.e[e] = (_Float16)fmaf((float)((u >> (8 * (e & 3))) & 0xffu), sv[e], nb[e]);
+          o.e[e] = q8_stage_f16((u >> (8 * (e & 3))) & 0xffu, sv[e]);
         }
         stv(vb + ((size_t)(vu * 4 + vpanel) * D + 4 * vdg + i) * 8, o.u);
       }

@@ -219,6 +219,33 @@ def test_segmented_prefill_equals_single(dev):
     c.close()
 
 
+@pytest.mark.parametrize("H,KV,D,gate", [(32, 8, 128, False), (24, 4, 256, True)])
+def test_q8_prefill_copy_matches_staging(dev, H, KV, D, gate):
+    """A q8 prefill of four or more query blocks runs on an f16 copy of the attended slots; the
+    copy holds exactly the values the q8 staging produces, so it must give the bit-identical
+    output of segments short enough (three blocks) to stage from the q8 cache directly."""
+    G = H // KV
+    QB = 128 // G
+    seg, nseg = 3 * QB, 4
+    S = seg * nseg
+    rng = np.random.default_rng(31 + D)
+    k = rng.standard_normal((S, KV, D)).astype(np.float32)
+    v = rng.standard_normal((S, KV, D)).astype(np.float32)
+    q = rng.standard_normal((S, H, D)).astype(np.float32)
+    g = rng.standard_normal((S, H, D)).astype(np.float32) if gate else None
+    c = E.KvCache(1, KV, D, "q8", max_seq_len=S, capacity=S)
+    fill_cache_raw(c, 0, k, v)
+    scale = 1.0 / np.sqrt(D)
+    whole = run_attention(c, 0, q, 0, scale=scale, gate=g)
+    parts = [run_attention(c, 0, q[i * seg:(i + 1) * seg], i * seg, scale=scale,
+                           gate=None if g is None else g[i * seg:(i + 1) * seg]) for i in range(nseg)]
+    assert np.array_equal(np.concatenate(parts), whole)
+    kk, vv = cached_values(c, 0, 0, S)
+    exp = ref.gated_attention(q, kk, vv, g, 0) if gate else ref.attention(q, kk, vv, 0, scale=scale)
+    _check("q8", whole, exp)
+    c.close()
+
+
 # ------------------------------------------------------------------ full-size configs
 def _norm_rope_case(cfg, S, past, seed, dtype=None):
     """Run the product path as the engine does: fused prologue for all positions, then
