@@ -14,7 +14,8 @@
  *   - A cache object is not re-entrant: calls on one cache must be serialized by the caller
  *     (the reference serializes every engine op through one promise chain, src/engine.ts:2877-2887).
  *   - Kernels never allocate. Host-side allocations happen only in bg_kv_create, bg_kv_grow and
- *     bg_attention_reserve (or lazily, once, on the first bg_attention that needs more workspace).
+ *     bg_attention_reserve (or lazily, once, on the first bg_attention that needs more workspace
+ *     or, for a q8 cache, the f16 copy a long prefill runs on).
  *
  * Storage modes mirror EngineOptions.kvCache (src/types.ts:143-154): f32, f16 (one RNE rounding
  * at write, shaders/copy_kv16.wgsl:13) and q8 (int8 codes + one f32 scale per 32 values,
@@ -153,7 +154,8 @@ int32_t bg_attention(bg_kv_cache* cache, int32_t layer, const float* q, int32_t 
                      float* out, void* stream);
 
 /* Pre-size the split-K workspace for up to S query rows of H heads (otherwise sized on first
- * use). Call before capturing bg_attention into a HIP graph. */
+ * use), and for a q8 cache whose prefill of S rows runs on an f16 copy of the attended slots,
+ * allocate that copy. Call before capturing bg_attention into a HIP graph. */
 int32_t bg_attention_reserve(bg_kv_cache* cache, int32_t S, int32_t H);
 
 /* ---- sink-mode eviction (overflow 'sinks') ------------------------------------------------
