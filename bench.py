@@ -41,9 +41,10 @@ def causal_flops(S, H, D, past=0):
     return 2 * 2 * D * H * (S * past + S * (S + 1) // 2)
 
 
-def graph_replay_us(torch, fn, steps, warmup):
-    """Capture fn() into a HIP graph; replay warmup times untimed, then time `steps` replays
-    bracketed by synchronize. Returns microseconds per replay."""
+def graph_replay_us(torch, fn, steps, warmup, per_graph=1):
+    """Capture fn() `per_graph` times back to back into one HIP graph; replay warmup times
+    untimed, then time `steps` replays bracketed by synchronize. Returns microseconds per fn()
+    (a graph that holds a single short launch would also time the graph launch itself)."""
     fn()
     torch.cuda.synchronize()
     s = torch.cuda.Stream()
@@ -53,7 +54,8 @@ def graph_replay_us(torch, fn, steps, warmup):
         fn()
         torch.cuda.synchronize()
         with torch.cuda.graph(g, stream=s):
-            fn()
+            for _ in range(per_graph):
+                fn()
     torch.cuda.synchronize()
     for _ in range(warmup):
         g.replay()
@@ -65,7 +67,7 @@ def graph_replay_us(torch, fn, steps, warmup):
         g.replay()
     e1.record()
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) * 1e3 / steps
+    return e0.elapsed_time(e1) * 1e3 / (steps * per_graph)
 
 
 class DecodeSweep:
@@ -175,8 +177,10 @@ def bench_prefill(torch, E, W, cfg, S, steps, warmup, seed):
                     out=out)
 
     prologue()
-    us_attn = graph_replay_us(torch, attn, steps, warmup)
-    us_pro = graph_replay_us(torch, prologue, steps, warmup)
+    # several launches per graph, as in a multi-layer prefill (one launch per layer)
+    per_graph = 8 if S <= 4096 else 2
+    us_attn = graph_replay_us(torch, attn, steps, warmup, per_graph)
+    us_pro = graph_replay_us(torch, prologue, steps, warmup, per_graph)
     fl = causal_flops(S, cfg.H, cfg.D)
     c.close()
     return {"S": S, "attn_us": round(us_attn, 1), "prologue_us": round(us_pro, 1),
@@ -250,7 +254,8 @@ def bench_c4(torch, E, W, steps, warmup):
         E.qkv_prologue(c, 0, None, k, v, fill + verify, cfg.H, None, ones, cfg.eps, cos, sin, cfg.rot, 0, 0)
         qr = E.qkv_prologue(c, 0, q, None, None, verify, cfg.H, ones, None, cfg.eps, cos, sin, cfg.rot, fill, fill)
         out = torch.empty(verify, cfg.H, cfg.D, device=dev)
-        us = graph_replay_us(torch, lambda: E.attention(c, 0, qr, verify, cfg.H, fill, out=out), steps, warmup)
+        us = graph_replay_us(torch, lambda: E.attention(c, 0, qr, verify, cfg.H, fill, out=out), steps, warmup,
+                             per_graph=16)
         B = (fill + verify) * cfg.KV * 2 * cfg.D * 2 + 2 * verify * cfg.H * cfg.D * 4
         res["decode" if verify == 1 else f"verify{verify}"] = {"us": round(us, 2), "GBs": round(B / us / 1e3, 1),
                                                                "resident_slots": fill + verify}
