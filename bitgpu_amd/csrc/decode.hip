@@ -320,6 +320,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
 #pragma unroll
     for (int i = 0; i < D / 16; i++) o[s][i] = floatx4{0, 0, 0, 0};
 
+  bool rescale = false;  // the last qk_softmax raised a reference max: pv rescales O first
   auto qk_softmax = [&](const TileRegs<D, DT, QUARTER>& T, int tile) {
     const int j0 = tile * 32;
     // ---------------- K operands ----------------
@@ -388,6 +389,9 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     }
 
     // ---------------- QK + online softmax, one pass per 4 query rows ----------------
+    // The reference max of a row is raised only when a tile's max exceeds it by more than 8 (in
+    // log2 units, so P <= 2^8 stays well inside f16); most tiles then leave O and l unscaled.
+    float xs[NPK][2], mts[NPK];
 #pragma unroll
     for (int pass = 0; pass < NPK; pass++) {
       if (pass >= NP) break;
@@ -442,13 +446,30 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
         const bool ok = row_ok && P < p.n_scan && P < p.phys_limit && Lg <= limit;
         x[t2] = ok ? sc[t2] : -INFINITY;
       }
-      const float mt = group16_max(fmaxf(x[0], x[1]));
-      const float mn = fmaxf(m[pass], mt);
-      const float corr = exp2f(m[pass] - mn);
-      const float p0 = exp2f(x[0] - mn), p1 = exp2f(x[1] - mn);
-      lsum[pass] = lsum[pass] * corr + p0 + p1;
-      m[pass] = mn;
-      if (n == 0 && rho < RS) cl[rho] = corr;
+      xs[pass][0] = x[0];
+      xs[pass][1] = x[1];
+      mts[pass] = group16_max(fmaxf(x[0], x[1]));
+    }
+    bool grow = false;
+#pragma unroll
+    for (int pass = 0; pass < NPK; pass++) {
+      if (pass >= NP) break;
+      grow = grow || mts[pass] > m[pass] + 8.0f;
+    }
+    rescale = __any(grow);
+#pragma unroll
+    for (int pass = 0; pass < NPK; pass++) {
+      if (pass >= NP) break;
+      const int rho = 4 * pass + g;
+      if (rescale) {
+        const float mn = fmaxf(m[pass], mts[pass]);
+        const float corr = exp2f(m[pass] - mn);
+        lsum[pass] *= corr;
+        m[pass] = mn;
+        if (n == 0 && rho < RS) cl[rho] = corr;
+      }
+      const float p0 = exp2f(xs[pass][0] - m[pass]), p1 = exp2f(xs[pass][1] - m[pass]);
+      lsum[pass] += p0 + p1;
       if (rho < RS) {
 #pragma unroll
         for (int t2 = 0; t2 < 2; t2++) {
@@ -481,9 +502,11 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     };
 #pragma unroll
     for (int st = 0; st < NSET; st++) {
-      const float cr = cl[16 * st + n];
+      if (rescale) {
+        const float cr = cl[16 * st + n];
 #pragma unroll
-      for (int i = 0; i < D / 16; i++) o[st][i] *= cr;
+        for (int i = 0; i < D / 16; i++) o[st][i] *= cr;
+      }
 #pragma unroll
       for (int b = 0; b < NB; b++) {
         H8 pb;
