@@ -20,10 +20,14 @@
 //             chunks XOR-swizzled by row so the MFMA operand reads hit distinct banks) and V^T
 //             (the cache's transposed 32-slot tiles, copied as they are) into LDS as f16,
 //             double-buffered with one barrier per step. An f16 cache is copied by the gfx950
-//             direct-to-LDS loads (global_load_lds_dwordx4: no registers, no VALU); q8 codes are
-//             dequantized (code * block scale / 127) and sink-mode keys rotated at their slot
-//             position through registers, once per workgroup. Either way the next step's loads
-//             are in flight while this step computes.
+//             direct-to-LDS buffer loads (buffer_load_dwordx4 ... lds: no registers, no VALU); q8
+//             codes are dequantized (code * block scale / 127) and sink-mode keys rotated at
+//             their slot position through registers, once per workgroup. Either way the next
+//             step's loads are in flight while this step computes.
+//   pipeline  D=256 with f16 tiles (one wave per SIMD): K is staged one step ahead of V and
+//             iteration s runs the QK MFMAs of step s+1 with the exp2 / f16 / row-sum work of step
+//             s between them, then the PV MFMAs of step s -- the VALU work hides under MFMAs
+//             instead of sitting between them.
 //   S^T = K Q^T  v_mfma_f32_32x32x16_f16, A = K from LDS, B = Q^T held in registers: a lane
 //             holds 16 keys of ONE row, so the softmax is lane-local plus one cross-half shuffle.
 //   softmax   base 2 with the hardware exp2 (results below 2^-126 flush to 0, as the f16 P
@@ -50,7 +54,6 @@ __device__ inline u32x4 ldv(const void* p) { return *(const u32x4*)p; }
 __device__ inline void stv(void* p, u32x4 v) { *(u32x4*)p = v; }
 
 typedef __attribute__((address_space(3))) void* lds_vptr;
-typedef __attribute__((address_space(1))) void* glb_vptr;
 
 union PH8 {
   half8p h;
@@ -116,7 +119,7 @@ struct Stager {
 
   __device__ explicit Stager(int t) {
     tt = t;
-    wt = t >> 6;
+    wt = __builtin_amdgcn_readfirstlane(t >> 6);  // uniform: the copies' LDS bases are scalars
     lane = t & 63;
     key = t / PH;
     cb = 16 * (t % PH);
@@ -126,30 +129,45 @@ struct Stager {
   }
 
   // f16 cache without rotation: this wave's 4 K and 4 V chunks of 64 lanes copied straight
-  // into LDS (the step's tiles are 4 waves x 4 x 64 chunks of 16 bytes each)
-  __device__ __forceinline__ void dma(const PrefillParams& p, int kvh, int j0, _Float16* kdst, _Float16* vdst) const {
-    const LayerView& L = p.L;
-    const int cap = L.cap;
-    const __half* kg = (const __half*)L.k + (size_t)kvh * cap * D;
-    const __half* vg = (const __half*)L.v + (size_t)kvh * cap * D;
+  // into LDS (the step's tiles are 4 waves x 4 x 64 chunks of 16 bytes each). The copies use the
+  // buffer form (a descriptor over the kv head's K or V region, a 32-bit lane offset): the
+  // compiler tracks those as vector-memory writes into one LDS array, whereas the global form
+  // counts as an access that may touch any LDS, after which every LDS read wait in the step
+  // becomes a wait for all outstanding reads.
+  __device__ __forceinline__ static __amdgpu_buffer_rsrc_t region(const void* base, int kvh, int cap) {
+    constexpr int kRawDwordFormat = 0x00020000;  // descriptor word 3: 32-bit data, raw access
+    return __builtin_amdgcn_make_buffer_rsrc((void*)((const char*)base + (size_t)kvh * cap * D * 2), (short)0,
+                                             cap * D * 2, kRawDwordFormat);
+  }
+  __device__ __forceinline__ void dma_k(const PrefillParams& p, int kvh, int j0, _Float16* kdst) const {
+    const int cap = p.L.cap;
+    const __amdgpu_buffer_rsrc_t rs = region(p.L.k, kvh, cap);
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const int pb = (4 * i + wt) * 64;   // first chunk position of this wave instruction
       const int P = pb + lane;
       const int r = P / C::CPR;
       const int c = (P % C::CPR) ^ (r & 15);
-      const __half* src = kg + (size_t)min(j0 + r, cap - 1) * D + c * 8;  // past the end: masked keys
-      __builtin_amdgcn_global_load_lds((glb_vptr)src, (lds_vptr)(kdst + pb * 8), 16, 0, 0);
+      const uint32_t off = (uint32_t)min(j0 + r, cap - 1) * (D * 2) + c * 16;  // past the end: masked keys
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_vptr)(kdst + pb * 8), 16, off, 0, 0, 0);
     }
+  }
+  __device__ __forceinline__ void dma_v(const PrefillParams& p, int kvh, int j0, _Float16* vdst) const {
+    const int cap = p.L.cap;
+    const __amdgpu_buffer_rsrc_t rs = region(p.L.v, kvh, cap);
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const int pb = (4 * i + wt) * 64;
       const int P = pb + lane;
       const int u = P / (4 * D);        // 32-slot tile of the chunk (4*D chunks per tile)
       const int tu = min((j0 >> 5) + u, cap / 32 - 1);
-      const __half* src = vg + (size_t)tu * 32 * D + (size_t)(P % (4 * D)) * 8;
-      __builtin_amdgcn_global_load_lds((glb_vptr)src, (lds_vptr)(vdst + pb * 8), 16, 0, 0);
+      const uint32_t off = (uint32_t)tu * (32 * D * 2) + (uint32_t)(P % (4 * D)) * 16;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_vptr)(vdst + pb * 8), 16, off, 0, 0, 0);
     }
+  }
+  __device__ __forceinline__ void dma(const PrefillParams& p, int kvh, int j0, _Float16* kdst, _Float16* vdst) const {
+    dma_k(p, kvh, j0, kdst);
+    dma_v(p, kvh, j0, vdst);
   }
 
   // register staging: issue the global loads of the step whose first key is slot j0
@@ -290,6 +308,9 @@ __global__ __launch_bounds__(256 * TEAMS) void prefill_kernel(PrefillParams p) {
   using C = PfCfg<D>;
   constexpr int KT = C::KT, NSUB = C::NSUB, NC = C::NC, ND = C::ND, TILE = C::TILE;
   constexpr bool DMA = DT == KV_F16 && !ROLL;
+  // software-pipelined steps where one wave per SIMD has nothing else to overlap with (D=256);
+  // with two teams the two waves of a SIMD already overlap one's softmax with the other's MFMAs
+  constexpr bool PIPE = DMA && TEAMS == 1;
   // Double buffers as four distinct arrays, [team][tile] each: the compiler then knows a DMA
   // into one buffer cannot alias the reads of the other, and adds no waits between them.
   __shared__ __align__(16) _Float16 lk0[TEAMS * TILE];
@@ -298,7 +319,7 @@ __global__ __launch_bounds__(256 * TEAMS) void prefill_kernel(PrefillParams p) {
   __shared__ __align__(16) _Float16 lv1[TEAMS * TILE];
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int team = TEAMS == 2 ? wave >> 2 : 0, wt = wave & 3;
   const int tt = tid & 255;  // thread index within the team
   const int g2 = lane >> 5, n = lane & 31;
@@ -380,7 +401,11 @@ __global__ __launch_bounds__(256 * TEAMS) void prefill_kernel(PrefillParams p) {
     // that step: the staging has no branches, so loads stay counted and registers registers.
     const int j00 = min(my_first, t_last) * KT;
     StageRegs<D, DT> R0;
-    if constexpr (DMA) {
+    if constexpr (PIPE) {
+      // K and V of the first step and K of the second (K is staged one step ahead of V)
+      stg.dma(p, kvh, j00, k0, v0);
+      stg.dma_k(p, kvh, min(my_first + 1, t_last) * KT, k1);
+    } else if constexpr (DMA) {
       stg.dma(p, kvh, j00, k0, v0);
     } else {
       stg.load(R0, p, kvh, j00);
@@ -391,8 +416,9 @@ __global__ __launch_bounds__(256 * TEAMS) void prefill_kernel(PrefillParams p) {
       return half8p{(_Float16)(a.x * sc), (_Float16)(a.y * sc), (_Float16)(a.z * sc), (_Float16)(a.w * sc),
                     (_Float16)(b.x * sc), (_Float16)(b.y * sc), (_Float16)(b.z * sc), (_Float16)(b.w * sc)};
     };
-    // operand area [row block][c][lane] of 16 bytes in the second buffer set (lk1, 32 KB)
-    _Float16* const qop = lk1;
+    // operand area [row block][c][lane] of 16 bytes in a buffer the first step does not fill
+    // (32 KB: lv1 when K is staged a step ahead, else lk1)
+    _Float16* const qop = PIPE ? lv1 : lk1;
     if constexpr (QLDS) {
 #pragma unroll
       for (int i = 0; i < 4; i++) {
@@ -426,9 +452,165 @@ __global__ __launch_bounds__(256 * TEAMS) void prefill_kernel(PrefillParams p) {
         hq.u = ldv(qop + (size_t)((wt * NC + c) * 64 + lane) * 8);
         qf[c] = hq.h;
       }
-      __syncthreads();  // every wave has its operand before step 0 stages into this buffer set
+      // every wave has its operand before the next staging into this buffer (with K staged a
+      // step ahead, the barrier after the first step's S covers it)
+      if constexpr (!PIPE) __syncthreads();
     }
 
+    if constexpr (PIPE) {
+      // ---------------- software-pipelined steps (f16 tiles copied straight into LDS) ----------------
+      // Iteration s: copy K of step s+2 and V of step s+1; S of step s+1 = K Q^T on the MFMAs while
+      // the VALU turns S of step s into P (exp2, f16, row sum); O += V P of step s; mask and max of
+      // S of step s+1. The MFMA pipe runs QK and PV back to back and the softmax VALU work runs
+      // under the QK MFMAs instead of between them. K buffers alternate s+1 (read) / s+2 (filled),
+      // V buffers s (read) / s+1 (filled).
+      constexpr int NA = NSUB == 1 ? 2 : NSUB;
+      float x[NSUB][16];  // S of the step whose P is computed next (masked, log2 units)
+      // S^T = K Q^T into sacc from the K tile at kc; with WITH_P, P of x is computed under it
+      auto qk = [&](auto with_p, const _Float16* kc, floatx16 (&sacc)[NA], PH8 (&pb)[NSUB][2]) {
+        constexpr bool WP = decltype(with_p)::value;
+#pragma unroll
+        for (int u = 0; u < NA; u++)
+#pragma unroll
+          for (int e = 0; e < 16; e++) sacc[u][e] = 0.0f;
+        PH8 ka[NC][NSUB];
+        auto rd = [&](int c) {
+#pragma unroll
+          for (int u = 0; u < NSUB; u++) ka[c][u].u = ldv(kc + k_chunk_pos<D>(u * 32 + n, 2 * c + g2) * 8);
+        };
+        // P of group g = (u, t): 8 exp2 of x, f16, row sum
+        const half2p ones = {(_Float16)1.0f, (_Float16)1.0f};
+        auto pgroup = [&](int g) {
+          const int u = g >> 1, t = g & 1;
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            pb[u][t].e[e] = (_Float16)__builtin_amdgcn_exp2f(x[u][8 * t + e] - m);
+            pb[u][t].e[4 + e] = (_Float16)__builtin_amdgcn_exp2f(x[u][8 * t + 4 + e] - m);
+          }
+#pragma unroll
+          for (int i = 0; i < 4; i++) lsum = __builtin_amdgcn_fdot2(pb[u][t].p[i], ones, lsum, false);
+        };
+        // in program order, each piece fenced: the reads of chunk c+2 ahead of chunk c's MFMAs,
+        // then a share of the P work (the scheduler left alone runs one accumulator chain first
+        // and waits for every read)
+        rd(0);
+        if (NC > 1) rd(1);
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+          if (c + 2 < NC) rd(c + 2);
+#pragma unroll
+          for (int u = 0; u < NSUB; u++) {
+            const int acc = NSUB == 1 ? (c & 1) : u;
+            sacc[acc] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[c][u].h, qf[c], sacc[acc], 0, 0, 0);
+          }
+          if constexpr (WP) {
+            // 2*NSUB groups of P over NC chunks
+            constexpr int GPC = (2 * NSUB + NC - 1) / NC;  // groups per chunk (>= 1)
+            constexpr int EVERY = NC / (2 * NSUB);         // chunks per group when fewer groups
+            if constexpr (EVERY >= 1) {
+              if (c % EVERY == EVERY - 1 && c / EVERY < 2 * NSUB) pgroup(c / EVERY);
+            } else {
+#pragma unroll
+              for (int k = 0; k < GPC; k++)
+                if (c * GPC + k < 2 * NSUB) pgroup(c * GPC + k);
+            }
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        // the accumulators are taken here, so no QK MFMA is sunk past this phase to its use
+#pragma unroll
+        for (int u = 0; u < NA; u++) asm volatile("" : "+v"(sacc[u]));
+        if constexpr (NSUB == 1) sacc[0] += sacc[1];
+      };
+      // mask S of step s1 into x and return its row max
+      auto mask_max = [&](int s1, const floatx16 (&sacc)[NA]) {
+        const bool live = s1 < my_count;
+        const int j0 = (my_first + (live ? s1 : 0)) * KT;
+        float mt = -INFINITY;
+        if (!live || j0 + KT > mask_from) {
+#pragma unroll
+          for (int u = 0; u < NSUB; u++)
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+#pragma unroll
+              for (int e = 0; e < 4; e++) {
+                const int P = j0 + 32 * u + 8 * k + 4 * g2 + e;
+                const bool ok = live && P < n_scan && P < p.phys_limit && P <= limit;
+                const float v = ok ? sacc[u][4 * k + e] : -INFINITY;
+                x[u][4 * k + e] = v;
+                mt = fmaxf(mt, v);
+              }
+        } else {
+#pragma unroll
+          for (int u = 0; u < NSUB; u++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+              x[u][e] = sacc[u][e];
+              mt = fmaxf(mt, x[u][e]);
+            }
+        }
+        const float2 r = pair32(mt);
+        return fmaxf(r.x, r.y);
+      };
+      // raise the reference max only when a step's max exceeds it by more than 2^8
+      auto raise = [&](float mt) {
+        const bool grow = mt > m + 8.0f;
+        if (__any(grow)) {
+          const float mn = grow ? mt : m;
+          const float corr = __builtin_amdgcn_exp2f(m - mn);
+          m = mn;
+          lsum *= corr;
+#pragma unroll
+          for (int i = 0; i < ND; i++) o[i] *= corr;
+        }
+      };
+      {
+        floatx16 sacc[NA];
+        PH8 pb[NSUB][2];
+        qk(std::false_type{}, k0, sacc, pb);
+        raise(mask_max(0, sacc));
+      }
+      __syncthreads();  // the first K buffer and the Q operand area are free
+
+      auto pstep = [&](int s, const _Float16* kn, const _Float16* vc, _Float16* kd, _Float16* vd) {
+        stg.dma_k(p, kvh, min(my_first + s + 2, t_last) * KT, kd);
+        stg.dma_v(p, kvh, min(my_first + s + 1, t_last) * KT, vd);
+        floatx16 sacc[NA];
+        PH8 pb[NSUB][2];
+        qk(std::true_type{}, kn, sacc, pb);
+        // (each phase's MFMAs stay in their phase: the schedule groups below would otherwise take
+        // the QK MFMAs of one 32-key half, and the reads feeding them, out of order)
+        __builtin_amdgcn_sched_barrier(0);
+        // O^T += V^T P^T of step s
+        PH8 va[2 * NSUB][ND];
+#pragma unroll
+        for (int ut = 0; ut < 2 * NSUB; ut++)
+#pragma unroll
+          for (int dc = 0; dc < ND; dc++)
+            va[ut][dc].u = ldv(vc + ((size_t)((ut >> 1) * 4 + 2 * (ut & 1) + g2) * D + 32 * dc + n) * 8);
+#pragma unroll
+        for (int u = 0; u < NSUB; u++)
+#pragma unroll
+          for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int dc = 0; dc < ND; dc++)
+              o[dc] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[2 * u + t][dc].h, pb[u][t].h, o[dc], 0, 0, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, ND, 0);
+#pragma unroll
+        for (int ut = 0; ut < 2 * NSUB - 1; ut++) {
+          __builtin_amdgcn_sched_group_barrier(0x100, ND, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, ND, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, ND, 0);
+        raise(mask_max(s + 1, sacc));
+        __builtin_amdgcn_s_waitcnt(0xf70);  // vmcnt(0): this wave's copies landed
+        __syncthreads();
+      };
+      for (int s = 0; s < steps; s += 2) {
+        pstep(s, k1, v0, k0, v1);
+        if (s + 1 < steps) pstep(s + 1, k0, v1, k1, v0);
+      }
+    } else {
     // ---------------- one step: stage step s+1 into (kn, vn), compute step s from (kc, vc) ----------------
     auto step = [&](int s, const _Float16* kc, const _Float16* vc, _Float16* kn, _Float16* vn) {
       const int jn = min(my_first + s + 1, t_last) * KT;
@@ -567,6 +749,7 @@ __global__ __launch_bounds__(256 * TEAMS) void prefill_kernel(PrefillParams p) {
     for (int s = 0; s < steps; s += 2) {
       step(s, k0, v0, k1, v1);
       if (s + 1 < steps) step(s + 1, k1, v1, k0, v0);
+    }
     }
 
     // ---------------- merge the two teams' states ----------------
