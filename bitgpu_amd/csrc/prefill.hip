@@ -77,6 +77,7 @@ struct PrefillParams {
   int n_qblocks;
   int n_scan_fixed;  // >0: scan this many physical slots for every block (sink mode after a wrap)
   int phys_limit;
+  int mirror;        // pair items heavy / light over the one wave of the grid (see the kernel)
 };
 
 template <int D>
@@ -303,317 +304,260 @@ struct Stager {
   }
 };
 
-template <int D, int DT, bool ROLL, int TEAMS>
-__global__ __launch_bounds__(256 * TEAMS) void prefill_kernel(PrefillParams p) {
+template <int D, int DT, bool ROLL>
+__global__ __launch_bounds__(256, D == 128 ? 2 : 1) void prefill_kernel(PrefillParams p) {
   using C = PfCfg<D>;
   constexpr int KT = C::KT, NSUB = C::NSUB, NC = C::NC, ND = C::ND, TILE = C::TILE;
   constexpr bool DMA = DT == KV_F16 && !ROLL;
-  // software-pipelined steps where one wave per SIMD has nothing else to overlap with (D=256);
-  // with two teams the two waves of a SIMD already overlap one's softmax with the other's MFMAs
-  constexpr bool PIPE = DMA && TEAMS == 1;
-  // Double buffers as four distinct arrays, [team][tile] each: the compiler then knows a DMA
-  // into one buffer cannot alias the reads of the other, and adds no waits between them.
-  __shared__ __align__(16) _Float16 lk0[TEAMS * TILE];
-  __shared__ __align__(16) _Float16 lk1[TEAMS * TILE];
-  __shared__ __align__(16) _Float16 lv0[TEAMS * TILE];
-  __shared__ __align__(16) _Float16 lv1[TEAMS * TILE];
+  // software-pipelined steps where a wave has its SIMD to itself (D=256: 512 registers a wave);
+  // D=128 runs two workgroups per CU, whose waves overlap one's softmax with the other's MFMAs
+  constexpr bool PIPE = DMA && D == 256;
+  // Double buffers as four distinct arrays: the compiler then knows a copy into one buffer cannot
+  // alias the reads of the other, and adds no waits between them. 64 KB: two workgroups a CU.
+  __shared__ __align__(16) _Float16 lk0[TILE];
+  __shared__ __align__(16) _Float16 lk1[TILE];
+  __shared__ __align__(16) _Float16 lv0[TILE];
+  __shared__ __align__(16) _Float16 lv1[TILE];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-  const int team = TEAMS == 2 ? wave >> 2 : 0, wt = wave & 3;
-  const int tt = tid & 255;  // thread index within the team
   const int g2 = lane >> 5, n = lane & 31;
   const int KV = p.L.kv_heads;
   const Ring ring = p.L.ring;
-  _Float16* const k0 = lk0 + team * TILE;
-  _Float16* const k1 = lk1 + team * TILE;
-  _Float16* const v0 = lv0 + team * TILE;
-  _Float16* const v1 = lv1 + team * TILE;
-  const Stager<D, DT, ROLL> stg(tt);
-  const int r = wt * 32 + n;  // this lane's row within the block
+  _Float16* const k0 = lk0;
+  _Float16* const k1 = lk1;
+  _Float16* const v0 = lv0;
+  _Float16* const v1 = lv1;
+  const Stager<D, DT, ROLL> stg(tid);
+  const int r = wave * 32 + n;  // this lane's row within the block
 
-  // Work items are (query block, kv head) pairs ordered heaviest (latest queries) first. With
-  // two teams (one workgroup per CU) the workgroup takes item blockIdx.x and its mirror
-  // n_items-1-blockIdx.x, so every workgroup scans about the same number of keys and the grid
-  // is one wave of workgroups; with one team the dispatcher balances one item per workgroup.
-  constexpr int ITEMS = TEAMS == 2 ? 2 : 1;
+  // Work items are (query block, kv head) pairs ordered heaviest (latest queries) first. A grid
+  // the CUs hold at once (mirror) pairs them: workgroup b < n/2 takes item b, the rest the mirrors
+  // n-1-(b-n/2), so that each CU holds one heavy and one light item and every CU scans about the
+  // same number of keys. A larger grid runs heaviest first, balanced by the dispatcher.
+  const int bid = blockIdx.x;
   const int n_items = p.n_qblocks * KV;
-  for (int it = 0; it < ITEMS; it++) {
-    const int item = it == 0 ? (int)blockIdx.x : n_items - 1 - (int)blockIdx.x;
-    if (it == 1 && item <= (int)blockIdx.x) break;  // odd count: the middle workgroup has one
-    const int kvh = item % KV;
-    const int qb = p.n_qblocks - 1 - item / KV;
-    const int s0 = qb * p.QB;
-    // G is laundered per item: row index math that depends only on the lane would otherwise be
-    // hoisted out of the item loop and held in registers through the whole step loop
-    int G = p.G;
-    asm volatile("" : "+s"(G));
+  const int half = (n_items + 1) / 2;
+  const int item = !p.mirror || bid < half ? bid : n_items - 1 - (bid - half);
+  const int kvh = item % KV;
+  const int qb = p.n_qblocks - 1 - item / KV;
+  const int s0 = qb * p.QB;
+  const int G = p.G;
 
-    const int qi = s0 + r / G;
-    const int h = kvh * G + r % G;
-    const bool row_ok = r < p.QB * p.G && qi < p.S;
-    const int limit = p.pos_base + qi;
+  const int qi = s0 + r / G;
+  const int h = kvh * G + r % G;
+  const bool row_ok = r < p.QB * p.G && qi < p.S;
+  const int limit = p.pos_base + qi;
 
-    // key range of the block, split into two equal halves with two teams (team 1 takes the
-    // larger one)
-    const int last_q = min(s0 + p.QB, p.S) - 1;
-    const int n_scan = p.n_scan_fixed > 0 ? p.n_scan_fixed : p.pos_base + last_q + 1;
-    const int T = (n_scan + KT - 1) / KT;
-    const int T0 = TEAMS == 2 ? T / 2 : 0;
-    const int my_first = team ? T0 : 0;
-    const int my_count = team || TEAMS == 1 ? T - T0 : T0;
-    const int steps = T - T0;
-    const int t_last = T - 1;
-    // the earliest key index any row of the block masks (causal diagonal or scan end)
-    const int mask_from = min(min(p.pos_base + s0 + 1, n_scan), p.phys_limit);
+  // key range of the block in KT-key steps
+  const int last_q = min(s0 + p.QB, p.S) - 1;
+  const int n_scan = p.n_scan_fixed > 0 ? p.n_scan_fixed : p.pos_base + last_q + 1;
+  const int steps = (n_scan + KT - 1) / KT;
+  const int t_last = steps - 1;
+  // the earliest key index any row of the block masks (causal diagonal or scan end)
+  const int mask_from = min(min(p.pos_base + s0 + 1, n_scan), p.phys_limit);
 
-    // ---------------- prologue: Q and the first tile, loads issued together ----------------
-    // Two teams (D=128): the block's 128 Q rows (f32, 64 KB) are read once per workgroup, as
-    // row-contiguous 32-byte pieces over all 512 threads, converted to the pre-scaled f16
-    // operand layout and put in the idle second buffer set; each wave then reads its Q^T
-    // operand from there. One team (D=256): each lane gathers its own operand.
-    constexpr bool QLDS = TEAMS == 2;
-    float4 qraw[QLDS ? 8 : 2 * NC];
-    int qunit[QLDS ? 4 : 1];
-    if constexpr (QLDS) {
-      int ln = tid, Gq = G;
-      asm volatile("" : "+v"(ln), "+s"(Gq));  // this lane math stays in the prologue
+  // ---------------- prologue: Q and the first tile, loads issued together ----------------
+  // each lane gathers its own Q^T operand (16 dims of one row per dim chunk)
+  float4 qraw[2 * NC];
+  {
+    const float* qr = p.q + ((size_t)(row_ok ? qi : 0) * p.H + (row_ok ? h : 0)) * D;
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int u = i * 512 + ln;   // 8-dim unit: row u / 16, dims 8 * (u % 16) ..
-        const int rr = u >> 4;
-        const int qq = s0 + rr / Gq, hh = kvh * Gq + rr % Gq;
-        const bool ok = rr < p.QB * Gq && qq < p.S;
-        const float* src = p.q + ((size_t)(ok ? qq : 0) * p.H + (ok ? hh : 0)) * D + 8 * (u & 15);
-        qraw[2 * i] = *(const float4*)src;
-        qraw[2 * i + 1] = *(const float4*)(src + 4);
-        qunit[i] = ok ? u : -1 - u;
-      }
-    } else {
-      const float* qr = p.q + ((size_t)(row_ok ? qi : 0) * p.H + (row_ok ? h : 0)) * D;
+    for (int c = 0; c < NC; c++) {
+      qraw[2 * c] = *(const float4*)(qr + 16 * c + 8 * g2);
+      qraw[2 * c + 1] = *(const float4*)(qr + 16 * c + 8 * g2 + 4);
+    }
+  }
+  const int j00 = 0;
+  StageRegs<D, DT> R0;
+  if constexpr (PIPE) {
+    // K and V of the first step and K of the second (K is staged one step ahead of V)
+    stg.dma(p, kvh, j00, k0, v0);
+    stg.dma_k(p, kvh, min(1, t_last) * KT, k1);
+  } else if constexpr (DMA) {
+    stg.dma(p, kvh, j00, k0, v0);
+  } else {
+    stg.load(R0, p, kvh, j00);
+  }
+  // Q^T operand: dims 16c + 8*g2 + [0..8), pre-scaled by scale*log2(e)
+  half8p qf[NC];
+  auto to_h8 = [](const float4& a, const float4& b, float sc) {
+    return half8p{(_Float16)(a.x * sc), (_Float16)(a.y * sc), (_Float16)(a.z * sc), (_Float16)(a.w * sc),
+                  (_Float16)(b.x * sc), (_Float16)(b.y * sc), (_Float16)(b.z * sc), (_Float16)(b.w * sc)};
+  };
+  {
+    const float sc = row_ok ? p.qscale : 0.0f;
+#pragma unroll
+    for (int c = 0; c < NC; c++) qf[c] = to_h8(qraw[2 * c], qraw[2 * c + 1], sc);
+  }
+  if constexpr (!DMA) stg.store(R0, p, j00, k0, v0);
+
+  floatx16 o[ND];
+#pragma unroll
+  for (int i = 0; i < ND; i++)
+#pragma unroll
+    for (int e = 0; e < 16; e++) o[i][e] = 0.0f;
+  float m = -1e30f, lsum = 0.0f;
+  if constexpr (DMA) __builtin_amdgcn_s_waitcnt(0xf70);  // vmcnt(0): this wave's copies landed
+  __syncthreads();
+
+  if constexpr (PIPE) {
+    // ---------------- software-pipelined steps (f16 tiles copied straight into LDS) ----------------
+    // Iteration s: copy K of step s+2 and V of step s+1; S of step s+1 = K Q^T on the MFMAs while
+    // the VALU turns S of step s into P (exp2, f16, row sum); O += V P of step s; mask and max of
+    // S of step s+1. The MFMA pipe runs QK and PV back to back and the softmax VALU work runs
+    // under the QK MFMAs instead of between them. K buffers alternate s+1 (read) / s+2 (filled),
+    // V buffers s (read) / s+1 (filled).
+    constexpr int NA = NSUB == 1 ? 2 : NSUB;
+    float x[NSUB][16];  // S of the step whose P is computed next (masked, log2 units)
+    // S^T = K Q^T into sacc from the K tile at kc; with WITH_P, P of x is computed under it
+    auto qk = [&](auto with_p, const _Float16* kc, floatx16 (&sacc)[NA], PH8 (&pb)[NSUB][2]) {
+      constexpr bool WP = decltype(with_p)::value;
+#pragma unroll
+      for (int u = 0; u < NA; u++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) sacc[u][e] = 0.0f;
+      PH8 ka[NC][NSUB];
+      auto rd = [&](int c) {
+#pragma unroll
+        for (int u = 0; u < NSUB; u++) ka[c][u].u = ldv(kc + k_chunk_pos<D>(u * 32 + n, 2 * c + g2) * 8);
+      };
+      // P of group g = (u, t): 8 exp2 of x, f16, row sum
+      const half2p ones = {(_Float16)1.0f, (_Float16)1.0f};
+      auto pgroup = [&](int g) {
+        const int u = g >> 1, t = g & 1;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          pb[u][t].e[e] = (_Float16)__builtin_amdgcn_exp2f(x[u][8 * t + e] - m);
+          pb[u][t].e[4 + e] = (_Float16)__builtin_amdgcn_exp2f(x[u][8 * t + 4 + e] - m);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) lsum = __builtin_amdgcn_fdot2(pb[u][t].p[i], ones, lsum, false);
+      };
+      // in program order, each piece fenced: the reads of chunk c+2 ahead of chunk c's MFMAs,
+      // then a share of the P work (the scheduler left alone runs one accumulator chain first
+      // and waits for every read)
+      rd(0);
+      if (NC > 1) rd(1);
 #pragma unroll
       for (int c = 0; c < NC; c++) {
-        qraw[2 * c] = *(const float4*)(qr + 16 * c + 8 * g2);
-        qraw[2 * c + 1] = *(const float4*)(qr + 16 * c + 8 * g2 + 4);
-      }
-    }
-    // A team past its last step re-stages a valid (clamped) tile into the buffer nobody reads
-    // that step: the staging has no branches, so loads stay counted and registers registers.
-    const int j00 = min(my_first, t_last) * KT;
-    StageRegs<D, DT> R0;
-    if constexpr (PIPE) {
-      // K and V of the first step and K of the second (K is staged one step ahead of V)
-      stg.dma(p, kvh, j00, k0, v0);
-      stg.dma_k(p, kvh, min(my_first + 1, t_last) * KT, k1);
-    } else if constexpr (DMA) {
-      stg.dma(p, kvh, j00, k0, v0);
-    } else {
-      stg.load(R0, p, kvh, j00);
-    }
-    // Q^T operand: dims 16c + 8*g2 + [0..8), pre-scaled by scale*log2(e)
-    half8p qf[NC];
-    auto to_h8 = [](const float4& a, const float4& b, float sc) {
-      return half8p{(_Float16)(a.x * sc), (_Float16)(a.y * sc), (_Float16)(a.z * sc), (_Float16)(a.w * sc),
-                    (_Float16)(b.x * sc), (_Float16)(b.y * sc), (_Float16)(b.z * sc), (_Float16)(b.w * sc)};
-    };
-    // operand area [row block][c][lane] of 16 bytes in a buffer the first step does not fill
-    // (32 KB: lv1 when K is staged a step ahead, else lk1)
-    _Float16* const qop = PIPE ? lv1 : lk1;
-    if constexpr (QLDS) {
+        if (c + 2 < NC) rd(c + 2);
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const bool ok = qunit[i] >= 0;
-        const int u = ok ? qunit[i] : -1 - qunit[i];
-        const int rr = u >> 4, j = u & 15;
-        const int at = ((rr >> 5) * NC + (j >> 1)) * 64 + (rr & 31) + 32 * (j & 1);
-        PH8 hq;
-        hq.h = to_h8(qraw[2 * i], qraw[2 * i + 1], ok ? p.qscale : 0.0f);
-        stv(qop + (size_t)at * 8, hq.u);
-      }
-    } else {
-      const float sc = row_ok ? p.qscale : 0.0f;
-#pragma unroll
-      for (int c = 0; c < NC; c++) qf[c] = to_h8(qraw[2 * c], qraw[2 * c + 1], sc);
-    }
-    if constexpr (!DMA) stg.store(R0, p, j00, k0, v0);
-
-    floatx16 o[ND];
-#pragma unroll
-    for (int i = 0; i < ND; i++)
-#pragma unroll
-      for (int e = 0; e < 16; e++) o[i][e] = 0.0f;
-    float m = -1e30f, lsum = 0.0f;
-    if constexpr (DMA) __builtin_amdgcn_s_waitcnt(0xf70);  // vmcnt(0): this wave's copies landed
-    __syncthreads();
-    if constexpr (QLDS) {
-#pragma unroll
-      for (int c = 0; c < NC; c++) {
-        PH8 hq;
-        hq.u = ldv(qop + (size_t)((wt * NC + c) * 64 + lane) * 8);
-        qf[c] = hq.h;
-      }
-      // every wave has its operand before the next staging into this buffer (with K staged a
-      // step ahead, the barrier after the first step's S covers it)
-      if constexpr (!PIPE) __syncthreads();
-    }
-
-    if constexpr (PIPE) {
-      // ---------------- software-pipelined steps (f16 tiles copied straight into LDS) ----------------
-      // Iteration s: copy K of step s+2 and V of step s+1; S of step s+1 = K Q^T on the MFMAs while
-      // the VALU turns S of step s into P (exp2, f16, row sum); O += V P of step s; mask and max of
-      // S of step s+1. The MFMA pipe runs QK and PV back to back and the softmax VALU work runs
-      // under the QK MFMAs instead of between them. K buffers alternate s+1 (read) / s+2 (filled),
-      // V buffers s (read) / s+1 (filled).
-      constexpr int NA = NSUB == 1 ? 2 : NSUB;
-      float x[NSUB][16];  // S of the step whose P is computed next (masked, log2 units)
-      // S^T = K Q^T into sacc from the K tile at kc; with WITH_P, P of x is computed under it
-      auto qk = [&](auto with_p, const _Float16* kc, floatx16 (&sacc)[NA], PH8 (&pb)[NSUB][2]) {
-        constexpr bool WP = decltype(with_p)::value;
-#pragma unroll
-        for (int u = 0; u < NA; u++)
-#pragma unroll
-          for (int e = 0; e < 16; e++) sacc[u][e] = 0.0f;
-        PH8 ka[NC][NSUB];
-        auto rd = [&](int c) {
-#pragma unroll
-          for (int u = 0; u < NSUB; u++) ka[c][u].u = ldv(kc + k_chunk_pos<D>(u * 32 + n, 2 * c + g2) * 8);
-        };
-        // P of group g = (u, t): 8 exp2 of x, f16, row sum
-        const half2p ones = {(_Float16)1.0f, (_Float16)1.0f};
-        auto pgroup = [&](int g) {
-          const int u = g >> 1, t = g & 1;
-#pragma unroll
-          for (int e = 0; e < 4; e++) {
-            pb[u][t].e[e] = (_Float16)__builtin_amdgcn_exp2f(x[u][8 * t + e] - m);
-            pb[u][t].e[4 + e] = (_Float16)__builtin_amdgcn_exp2f(x[u][8 * t + 4 + e] - m);
-          }
-#pragma unroll
-          for (int i = 0; i < 4; i++) lsum = __builtin_amdgcn_fdot2(pb[u][t].p[i], ones, lsum, false);
-        };
-        // in program order, each piece fenced: the reads of chunk c+2 ahead of chunk c's MFMAs,
-        // then a share of the P work (the scheduler left alone runs one accumulator chain first
-        // and waits for every read)
-        rd(0);
-        if (NC > 1) rd(1);
-#pragma unroll
-        for (int c = 0; c < NC; c++) {
-          if (c + 2 < NC) rd(c + 2);
-#pragma unroll
-          for (int u = 0; u < NSUB; u++) {
-            const int acc = NSUB == 1 ? (c & 1) : u;
-            sacc[acc] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[c][u].h, qf[c], sacc[acc], 0, 0, 0);
-          }
-          if constexpr (WP) {
-            // 2*NSUB groups of P over NC chunks
-            constexpr int GPC = (2 * NSUB + NC - 1) / NC;  // groups per chunk (>= 1)
-            constexpr int EVERY = NC / (2 * NSUB);         // chunks per group when fewer groups
-            if constexpr (EVERY >= 1) {
-              if (c % EVERY == EVERY - 1 && c / EVERY < 2 * NSUB) pgroup(c / EVERY);
-            } else {
-#pragma unroll
-              for (int k = 0; k < GPC; k++)
-                if (c * GPC + k < 2 * NSUB) pgroup(c * GPC + k);
-            }
-          }
-          __builtin_amdgcn_sched_barrier(0);
+        for (int u = 0; u < NSUB; u++) {
+          const int acc = NSUB == 1 ? (c & 1) : u;
+          sacc[acc] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[c][u].h, qf[c], sacc[acc], 0, 0, 0);
         }
-        // the accumulators are taken here, so no QK MFMA is sunk past this phase to its use
+        if constexpr (WP) {
+          // 2*NSUB groups of P over NC chunks
+          constexpr int GPC = (2 * NSUB + NC - 1) / NC;  // groups per chunk (>= 1)
+          constexpr int EVERY = NC / (2 * NSUB);         // chunks per group when fewer groups
+          if constexpr (EVERY >= 1) {
+            if (c % EVERY == EVERY - 1 && c / EVERY < 2 * NSUB) pgroup(c / EVERY);
+          } else {
 #pragma unroll
-        for (int u = 0; u < NA; u++) asm volatile("" : "+v"(sacc[u]));
-        if constexpr (NSUB == 1) sacc[0] += sacc[1];
-      };
-      // mask S of step s1 into x and return its row max
-      auto mask_max = [&](int s1, const floatx16 (&sacc)[NA]) {
-        const bool live = s1 < my_count;
-        const int j0 = (my_first + (live ? s1 : 0)) * KT;
-        float mt = -INFINITY;
-        if (!live || j0 + KT > mask_from) {
-#pragma unroll
-          for (int u = 0; u < NSUB; u++)
-#pragma unroll
-            for (int k = 0; k < 4; k++)
-#pragma unroll
-              for (int e = 0; e < 4; e++) {
-                const int P = j0 + 32 * u + 8 * k + 4 * g2 + e;
-                const bool ok = live && P < n_scan && P < p.phys_limit && P <= limit;
-                const float v = ok ? sacc[u][4 * k + e] : -INFINITY;
-                x[u][4 * k + e] = v;
-                mt = fmaxf(mt, v);
-              }
-        } else {
-#pragma unroll
-          for (int u = 0; u < NSUB; u++)
-#pragma unroll
-            for (int e = 0; e < 16; e++) {
-              x[u][e] = sacc[u][e];
-              mt = fmaxf(mt, x[u][e]);
-            }
+            for (int k = 0; k < GPC; k++)
+              if (c * GPC + k < 2 * NSUB) pgroup(c * GPC + k);
+          }
         }
-        const float2 r = pair32(mt);
-        return fmaxf(r.x, r.y);
-      };
-      // raise the reference max only when a step's max exceeds it by more than 2^8
-      auto raise = [&](float mt) {
-        const bool grow = mt > m + 8.0f;
-        if (__any(grow)) {
-          const float mn = grow ? mt : m;
-          const float corr = __builtin_amdgcn_exp2f(m - mn);
-          m = mn;
-          lsum *= corr;
-#pragma unroll
-          for (int i = 0; i < ND; i++) o[i] *= corr;
-        }
-      };
-      {
-        floatx16 sacc[NA];
-        PH8 pb[NSUB][2];
-        qk(std::false_type{}, k0, sacc, pb);
-        raise(mask_max(0, sacc));
-      }
-      __syncthreads();  // the first K buffer and the Q operand area are free
-
-      auto pstep = [&](int s, const _Float16* kn, const _Float16* vc, _Float16* kd, _Float16* vd) {
-        stg.dma_k(p, kvh, min(my_first + s + 2, t_last) * KT, kd);
-        stg.dma_v(p, kvh, min(my_first + s + 1, t_last) * KT, vd);
-        floatx16 sacc[NA];
-        PH8 pb[NSUB][2];
-        qk(std::true_type{}, kn, sacc, pb);
-        // (each phase's MFMAs stay in their phase: the schedule groups below would otherwise take
-        // the QK MFMAs of one 32-key half, and the reads feeding them, out of order)
         __builtin_amdgcn_sched_barrier(0);
-        // O^T += V^T P^T of step s
-        PH8 va[2 * NSUB][ND];
+      }
+      // the accumulators are taken here, so no QK MFMA is sunk past this phase to its use
 #pragma unroll
-        for (int ut = 0; ut < 2 * NSUB; ut++)
-#pragma unroll
-          for (int dc = 0; dc < ND; dc++)
-            va[ut][dc].u = ldv(vc + ((size_t)((ut >> 1) * 4 + 2 * (ut & 1) + g2) * D + 32 * dc + n) * 8);
+      for (int u = 0; u < NA; u++) asm volatile("" : "+v"(sacc[u]));
+      if constexpr (NSUB == 1) sacc[0] += sacc[1];
+    };
+    // mask S of step s1 into x and return its row max
+    auto mask_max = [&](int s1, const floatx16 (&sacc)[NA]) {
+      const bool live = s1 < steps;  // the look-ahead past the last step is all masked
+      const int j0 = (live ? s1 : 0) * KT;
+      float mt = -INFINITY;
+      if (!live || j0 + KT > mask_from) {
 #pragma unroll
         for (int u = 0; u < NSUB; u++)
 #pragma unroll
-          for (int t = 0; t < 2; t++)
+          for (int k = 0; k < 4; k++)
 #pragma unroll
-            for (int dc = 0; dc < ND; dc++)
-              o[dc] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[2 * u + t][dc].h, pb[u][t].h, o[dc], 0, 0, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, ND, 0);
+            for (int e = 0; e < 4; e++) {
+              const int P = j0 + 32 * u + 8 * k + 4 * g2 + e;
+              const bool ok = live && P < n_scan && P < p.phys_limit && P <= limit;
+              const float v = ok ? sacc[u][4 * k + e] : -INFINITY;
+              x[u][4 * k + e] = v;
+              mt = fmaxf(mt, v);
+            }
+      } else {
 #pragma unroll
-        for (int ut = 0; ut < 2 * NSUB - 1; ut++) {
-          __builtin_amdgcn_sched_group_barrier(0x100, ND, 0);
-          __builtin_amdgcn_sched_group_barrier(0x008, ND, 0);
-        }
-        __builtin_amdgcn_sched_group_barrier(0x008, ND, 0);
-        raise(mask_max(s + 1, sacc));
-        __builtin_amdgcn_s_waitcnt(0xf70);  // vmcnt(0): this wave's copies landed
-        __syncthreads();
-      };
-      for (int s = 0; s < steps; s += 2) {
-        pstep(s, k1, v0, k0, v1);
-        if (s + 1 < steps) pstep(s + 1, k0, v1, k1, v0);
+        for (int u = 0; u < NSUB; u++)
+#pragma unroll
+          for (int e = 0; e < 16; e++) {
+            x[u][e] = sacc[u][e];
+            mt = fmaxf(mt, x[u][e]);
+          }
       }
-    } else {
+      const float2 r = pair32(mt);
+      return fmaxf(r.x, r.y);
+    };
+    // raise the reference max only when a step's max exceeds it by more than 2^8
+    auto raise = [&](float mt) {
+      const bool grow = mt > m + 8.0f;
+      if (__any(grow)) {
+        const float mn = grow ? mt : m;
+        const float corr = __builtin_amdgcn_exp2f(m - mn);
+        m = mn;
+        lsum *= corr;
+#pragma unroll
+        for (int i = 0; i < ND; i++) o[i] *= corr;
+      }
+    };
+    {
+      floatx16 sacc[NA];
+      PH8 pb[NSUB][2];
+      qk(std::false_type{}, k0, sacc, pb);
+      raise(mask_max(0, sacc));
+    }
+    __syncthreads();  // the first K buffer and the Q operand area are free
+
+    auto pstep = [&](int s, const _Float16* kn, const _Float16* vc, _Float16* kd, _Float16* vd) {
+      stg.dma_k(p, kvh, min(s + 2, t_last) * KT, kd);
+      stg.dma_v(p, kvh, min(s + 1, t_last) * KT, vd);
+      floatx16 sacc[NA];
+      PH8 pb[NSUB][2];
+      qk(std::true_type{}, kn, sacc, pb);
+      // (each phase's MFMAs stay in their phase: the schedule groups below would otherwise take
+      // the QK MFMAs of one 32-key half, and the reads feeding them, out of order)
+      __builtin_amdgcn_sched_barrier(0);
+      // O^T += V^T P^T of step s
+      PH8 va[2 * NSUB][ND];
+#pragma unroll
+      for (int ut = 0; ut < 2 * NSUB; ut++)
+#pragma unroll
+        for (int dc = 0; dc < ND; dc++)
+          va[ut][dc].u = ldv(vc + ((size_t)((ut >> 1) * 4 + 2 * (ut & 1) + g2) * D + 32 * dc + n) * 8);
+#pragma unroll
+      for (int u = 0; u < NSUB; u++)
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+          for (int dc = 0; dc < ND; dc++)
+            o[dc] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[2 * u + t][dc].h, pb[u][t].h, o[dc], 0, 0, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, ND, 0);
+#pragma unroll
+      for (int ut = 0; ut < 2 * NSUB - 1; ut++) {
+        __builtin_amdgcn_sched_group_barrier(0x100, ND, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, ND, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, ND, 0);
+      raise(mask_max(s + 1, sacc));
+      __builtin_amdgcn_s_waitcnt(0xf70);  // vmcnt(0): this wave's copies landed
+      __syncthreads();
+    };
+    for (int s = 0; s < steps; s += 2) {
+      pstep(s, k1, v0, k0, v1);
+      if (s + 1 < steps) pstep(s + 1, k0, v1, k1, v0);
+    }
+  } else {
     // ---------------- one step: stage step s+1 into (kn, vn), compute step s from (kc, vc) ----------------
     auto step = [&](int s, const _Float16* kc, const _Float16* vc, _Float16* kn, _Float16* vn) {
-      const int jn = min(my_first + s + 1, t_last) * KT;
+      const int jn = min(s + 1, t_last) * KT;
       StageRegs<D, DT> R;
       if constexpr (DMA) {
         stg.dma(p, kvh, jn, kn, vn);
@@ -624,10 +568,7 @@ __global__ __launch_bounds__(256 * TEAMS) void prefill_kernel(PrefillParams p) {
         __builtin_amdgcn_sched_barrier(0);
       }
 
-      // a team past its last step computes on a fully masked tile (no branch around the
-      // compute, which would let the loads above sink)
-      const bool live = s < my_count;
-      const int j0 = (my_first + (live ? s : 0)) * KT;
+      const int j0 = s * KT;
       // S^T = K Q^T
       // one 32-key sub-tile (D=256): two accumulators over even / odd dim chunks, so the QK
       // MFMAs form two independent chains
@@ -667,7 +608,7 @@ __global__ __launch_bounds__(256 * TEAMS) void prefill_kernel(PrefillParams p) {
       // mask + online softmax (row = this lane's n)
       float x[NSUB][16];
       float mt = -INFINITY;
-      if (ROLL || !live || j0 + KT > mask_from) {
+      if (ROLL || j0 + KT > mask_from) {
 #pragma unroll
         for (int u = 0; u < NSUB; u++)
 #pragma unroll
@@ -676,7 +617,7 @@ __global__ __launch_bounds__(256 * TEAMS) void prefill_kernel(PrefillParams p) {
             for (int e = 0; e < 4; e++) {
               const int P = j0 + 32 * u + 8 * k + 4 * g2 + e;
               const int Lg = ROLL ? ring.logical(P) : P;
-              const bool ok = live && P < n_scan && P < p.phys_limit && Lg <= limit;
+              const bool ok = P < n_scan && P < p.phys_limit && Lg <= limit;
               const float v = ok ? sacc[u][4 * k + e] : -INFINITY;
               x[u][4 * k + e] = v;
               mt = fmaxf(mt, v);
@@ -750,113 +691,87 @@ __global__ __launch_bounds__(256 * TEAMS) void prefill_kernel(PrefillParams p) {
       step(s, k0, v0, k1, v1);
       if (s + 1 < steps) step(s + 1, k1, v1, k0, v0);
     }
-    }
+  }
 
-    // ---------------- merge the two teams' states ----------------
-    if constexpr (TEAMS == 2) {
-      // team 1's O (64 floats a lane) in lk0|lk1, its m and l in lv0: [wt][slot][lane]
-      float* mo = (float*)(wt < 2 ? lk0 : lk1) + (size_t)(wt & 1) * ND * 16 * 64 + lane;
-      float* ml = (float*)lv0 + (size_t)wt * 2 * 64 + lane;
-      if (team == 1) {
+  // ---------------- store ----------------
+  {
+    { const float2 r = pair32(lsum); lsum = r.x + r.y; }
+    if constexpr (D == 128) {
+      // through one LDS array per wave (16 KB, the tiles are no longer read): rows written
+      // swizzled, read back and stored as contiguous 512-byte rows (the register layout
+      // scatters 16 bytes per row)
+      float4* rows = (float4*)(wave == 0 ? lk0 : wave == 1 ? lk1 : wave == 2 ? lv0 : lv1);
+      // lane and G laundered: the swizzled addresses below are computed here, not at the
+      // kernel start (where they would be held, or spilled, through the step loop)
+      int ln = lane, Ge = G;
+      asm volatile("" : "+v"(ln), "+s"(Ge));
+      const int en = ln & 31, eg = ln >> 5;
+      const float inv = 1.0f / lsum;
+      if (p.gate) {  // the gate divides o / l first (gate_sigmoid.wgsl:13 on the normalized row)
 #pragma unroll
         for (int dc = 0; dc < ND; dc++)
 #pragma unroll
-          for (int e = 0; e < 16; e++) mo[(dc * 16 + e) * 64] = o[dc][e];
-        ml[0] = m;
-        ml[64] = lsum;
+          for (int k = 0; k < 4; k++)
+            rows[en * 32 + ((8 * dc + 2 * k + eg) ^ en)] =
+                make_float4(o[dc][4 * k] / lsum, o[dc][4 * k + 1] / lsum, o[dc][4 * k + 2] / lsum, o[dc][4 * k + 3] / lsum);
+      } else {
+#pragma unroll
+        for (int dc = 0; dc < ND; dc++)
+#pragma unroll
+          for (int k = 0; k < 4; k++)
+            rows[en * 32 + ((8 * dc + 2 * k + eg) ^ en)] =
+                make_float4(o[dc][4 * k] * inv, o[dc][4 * k + 1] * inv, o[dc][4 * k + 2] * inv, o[dc][4 * k + 3] * inv);
       }
-      __syncthreads();
-      if (team == 0) {
-        const float m1 = ml[0], l1 = ml[64];
-        const float M = fmaxf(m, m1);
-        const float a0 = exp2f(m - M), a1 = exp2f(m1 - M);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const int cl = en;
+      auto emit = [&](auto gated) {
 #pragma unroll
-        for (int dc = 0; dc < ND; dc++)
-#pragma unroll
-          for (int e = 0; e < 16; e++) o[dc][e] = o[dc][e] * a0 + mo[(dc * 16 + e) * 64] * a1;
-        lsum = lsum * a0 + l1 * a1;
-      }
-    }
-    // ---------------- store ----------------
-    if (team == 0) {
-      { const float2 r = pair32(lsum); lsum = r.x + r.y; }
-      if constexpr (TEAMS == 2) {
-        // through this wave's own merge region: rows written swizzled, read back and stored as
-        // contiguous 512-byte rows (the register layout scatters 16 bytes per row)
-        float4* rows = (float4*)((float*)(wt < 2 ? lk0 : lk1) + (size_t)(wt & 1) * ND * 16 * 64);
-        // lane and G laundered: the swizzled addresses below are computed here, not at the
-        // kernel start (where they would be held, or spilled, through the step loop)
-        int ln = lane, Ge = G;
-        asm volatile("" : "+v"(ln), "+s"(Ge));
-        const int en = ln & 31, eg = ln >> 5;
-        const float inv = 1.0f / lsum;
-        if (p.gate) {  // the gate divides o / l first (gate_sigmoid.wgsl:13 on the normalized row)
-#pragma unroll
-          for (int dc = 0; dc < ND; dc++)
-#pragma unroll
-            for (int k = 0; k < 4; k++)
-              rows[en * 32 + ((8 * dc + 2 * k + eg) ^ en)] =
-                  make_float4(o[dc][4 * k] / lsum, o[dc][4 * k + 1] / lsum, o[dc][4 * k + 2] / lsum, o[dc][4 * k + 3] / lsum);
-        } else {
-#pragma unroll
-          for (int dc = 0; dc < ND; dc++)
-#pragma unroll
-            for (int k = 0; k < 4; k++)
-              rows[en * 32 + ((8 * dc + 2 * k + eg) ^ en)] =
-                  make_float4(o[dc][4 * k] * inv, o[dc][4 * k + 1] * inv, o[dc][4 * k + 2] * inv, o[dc][4 * k + 3] * inv);
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        const int cl = en;
-        auto emit = [&](auto gated) {
-#pragma unroll
-          for (int i = 0; i < 16; i++) {
-            const int rl = 2 * i + eg;                 // row within the wave
-            const int rb = wt * 32 + rl;               // row within the block
-            const int qq = s0 + rb / Ge, hh = kvh * Ge + rb % Ge;
-            float4 v = rows[rl * 32 + (cl ^ (rl & 31))];
-            if (rb < p.QB * Ge && qq < p.S) {
-              if constexpr (decltype(gated)::value) {
-                // gate_sigmoid.wgsl:13 form: x / (1 + exp(-g))
-                const float4 gv = *(const float4*)(p.gate + ((size_t)qq * p.H + hh) * p.gate_stride + 4 * cl);
-                v.x = v.x / (1.0f + expf(-gv.x));
-                v.y = v.y / (1.0f + expf(-gv.y));
-                v.z = v.z / (1.0f + expf(-gv.z));
-                v.w = v.w / (1.0f + expf(-gv.w));
-              }
-              *(float4*)(p.out + ((size_t)qq * p.H + hh) * D + 4 * cl) = v;
-            }
-          }
-        };
-        if (p.gate) emit(std::true_type{});
-        else emit(std::false_type{});
-      } else if (row_ok) {
-        const float inv = 1.0f / lsum;
-        float* orow = p.out + ((size_t)qi * p.H + h) * D;
-        const float* grow_ = p.gate ? p.gate + ((size_t)qi * p.H + h) * p.gate_stride : nullptr;
-#pragma unroll
-        for (int dc = 0; dc < ND; dc++)
-#pragma unroll
-          for (int k = 0; k < 4; k++) {
-            const int d = 32 * dc + 8 * k + 4 * g2;
-            float4 v;
-            v.x = o[dc][4 * k + 0] * inv;
-            v.y = o[dc][4 * k + 1] * inv;
-            v.z = o[dc][4 * k + 2] * inv;
-            v.w = o[dc][4 * k + 3] * inv;
-            if (grow_) {
+        for (int i = 0; i < 16; i++) {
+          const int rl = 2 * i + eg;                 // row within the wave
+          const int rb = wave * 32 + rl;               // row within the block
+          const int qq = s0 + rb / Ge, hh = kvh * Ge + rb % Ge;
+          float4 v = rows[rl * 32 + (cl ^ (rl & 31))];
+          if (rb < p.QB * Ge && qq < p.S) {
+            if constexpr (decltype(gated)::value) {
               // gate_sigmoid.wgsl:13 form: x / (1 + exp(-g))
-              v.x = (o[dc][4 * k + 0] / lsum) / (1.0f + expf(-grow_[d + 0]));
-              v.y = (o[dc][4 * k + 1] / lsum) / (1.0f + expf(-grow_[d + 1]));
-              v.z = (o[dc][4 * k + 2] / lsum) / (1.0f + expf(-grow_[d + 2]));
-              v.w = (o[dc][4 * k + 3] / lsum) / (1.0f + expf(-grow_[d + 3]));
+              const float4 gv = *(const float4*)(p.gate + ((size_t)qq * p.H + hh) * p.gate_stride + 4 * cl);
+              v.x = v.x / (1.0f + expf(-gv.x));
+              v.y = v.y / (1.0f + expf(-gv.y));
+              v.z = v.z / (1.0f + expf(-gv.z));
+              v.w = v.w / (1.0f + expf(-gv.w));
             }
-            *(float4*)(orow + d) = v;
+            *(float4*)(p.out + ((size_t)qq * p.H + hh) * D + 4 * cl) = v;
           }
-      }
+        }
+      };
+      if (p.gate) emit(std::true_type{});
+      else emit(std::false_type{});
+    } else if (row_ok) {
+      const float inv = 1.0f / lsum;
+      float* orow = p.out + ((size_t)qi * p.H + h) * D;
+      const float* grow_ = p.gate ? p.gate + ((size_t)qi * p.H + h) * p.gate_stride : nullptr;
+#pragma unroll
+      for (int dc = 0; dc < ND; dc++)
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          const int d = 32 * dc + 8 * k + 4 * g2;
+          float4 v;
+          v.x = o[dc][4 * k + 0] * inv;
+          v.y = o[dc][4 * k + 1] * inv;
+          v.z = o[dc][4 * k + 2] * inv;
+          v.w = o[dc][4 * k + 3] * inv;
+          if (grow_) {
+            // gate_sigmoid.wgsl:13 form: x / (1 + exp(-g))
+            v.x = (o[dc][4 * k + 0] / lsum) / (1.0f + expf(-grow_[d + 0]));
+            v.y = (o[dc][4 * k + 1] / lsum) / (1.0f + expf(-grow_[d + 1]));
+            v.z = (o[dc][4 * k + 2] / lsum) / (1.0f + expf(-grow_[d + 2]));
+            v.w = (o[dc][4 * k + 3] / lsum) / (1.0f + expf(-grow_[d + 3]));
+          }
+          *(float4*)(orow + d) = v;
+        }
     }
-    __syncthreads();  // the merge area is the next item's staging buffers
   }
 }
 
@@ -876,14 +791,17 @@ bool prefill_wants_f16_copy(const LayerView& L, int S, int H) {
   return (S + QB - 1) / QB >= 4;
 }
 
-// two teams where the registers allow two waves per SIMD (D=128); D=256 keeps its O and Q^T in
-// one wave per SIMD's 512 registers
+// D=128 runs two workgroups a CU (64 KB of LDS and 256 registers a wave each). A D=128 grid that
+// fits at once is dispatched as one wave, the first half of the workgroups one a CU and the second
+// half beside them, so pairing item b with its mirror (see the kernel) pairs heavy and light items
+// on each CU. Other grids (D=256: one workgroup a CU) run heaviest first, balanced by the
+// dispatcher.
+static bool pf_mirror(const LayerView& L, int n_items, int num_cus) { return L.D == 128 && n_items <= 2 * num_cus; }
+
 template <int D, int DT, bool ROLL>
 static hipError_t launch_pf(const PrefillParams& p, hipStream_t st) {
-  constexpr int TEAMS = D == 128 ? 2 : 1;
-  const int n_items = p.n_qblocks * p.L.kv_heads;
-  const int n_wg = TEAMS == 2 ? (n_items + 1) / 2 : n_items;
-  hipLaunchKernelGGL((prefill_kernel<D, DT, ROLL, TEAMS>), dim3(n_wg), dim3(256 * TEAMS), 0, st, p);
+  const int n_wg = p.n_qblocks * p.L.kv_heads;
+  hipLaunchKernelGGL((prefill_kernel<D, DT, ROLL>), dim3(n_wg), dim3(256), 0, st, p);
   return hipGetLastError();
 }
 
@@ -903,6 +821,7 @@ hipError_t launch_attention_prefill(const LayerView& L, const AttnArgs& a, hipSt
   p.n_qblocks = (a.S + p.QB - 1) / p.QB;
   p.n_scan_fixed = (L.ring.roll && L.ring.head != 0) ? L.max_seq : 0;
   p.phys_limit = L.ring.roll ? L.max_seq : L.cap;
+  p.mirror = pf_mirror(L, p.n_qblocks * L.kv_heads, a.num_cus);
   const bool roll = L.ring.roll != 0;
   if (L.D == 128) {
     if (L.dtype == KV_Q8) return roll ? launch_pf<128, KV_Q8, true>(p, st) : launch_pf<128, KV_Q8, false>(p, st);
