@@ -5,18 +5,16 @@
 // subgroup or workgroup per (query, head) with a serial key loop. Here prefill is a dense
 // contraction:
 //   rows      a row is a (query, head) pair; the G heads of one kv head are packed into the rows
-//             so every staged K/V byte serves G heads. A wave owns 32 rows, a team of 4 waves 128.
-//   teams     D=128: a workgroup is 8 waves = two teams of 4. Both teams hold the same 128 rows;
-//             team 0 scans the first half of the block's key range, team 1 the second half, and
-//             the two online-softmax states are merged through LDS at the end. Two waves per
-//             SIMD (one of each team) let one wave's softmax overlap the other's MFMAs, and the
-//             halves are equal so neither team idles. D=256 keeps one team of 4 waves, each with
-//             a full SIMD's registers.
-//   items     D=128: a workgroup processes a heavy query block (late queries, long key range)
-//             and its mirror light block, so all workgroups do about the same work in one wave
-//             of the grid -- no causal tail, no dispatch gaps. D=256: one block per workgroup,
-//             heaviest first, balanced by the dispatcher.
-//   staging   per step a team stages KT keys (64 for D=128, 32 for D=256) of K (row-major, 16-byte
+//             so every staged K/V byte serves G heads. A wave owns 32 rows, a workgroup of 4
+//             waves one query block of 128 rows, over the block's whole key range.
+//   occupancy D=128: 64 KB of LDS and at most 256 registers a wave, so two workgroups share a
+//             CU; their waves meet no common barrier, so one's softmax overlaps the other's
+//             MFMAs. D=256: one workgroup a CU, each wave with a full SIMD's 512 registers.
+//   items     (query block, kv head) pairs, heaviest (latest queries) first. A D=128 grid that
+//             fits at once pairs each heavy item with its mirror light item on one CU, so all
+//             CUs scan about the same number of keys; other grids are balanced by the
+//             dispatcher.
+//   staging   per step a workgroup stages KT keys (64 for D=128, 32 for D=256) of K (row-major, 16-byte
 //             chunks XOR-swizzled by row so the MFMA operand reads hit distinct banks) and V^T
 //             (the cache's transposed 32-slot tiles, copied as they are) into LDS as f16,
 //             double-buffered with one barrier per step. An f16 cache is copied by the gfx950
