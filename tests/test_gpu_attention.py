@@ -196,6 +196,33 @@ def test_prefill_shapes(dev, dtype, S, past):
     _check(dtype, out, exp)
 
 
+@pytest.mark.parametrize("H,KV,S", [(4, 1, 96), (12, 3, 160)])
+def test_prefill_odd_item_count(dev, H, KV, S):
+    """A D=128 grid that fits the CUs at once pairs item b with its mirror n-1-b; with an odd
+    item count the middle workgroup has none."""
+    out, exp = _raw_case("f16", H, KV, 128, S, S, seed=H * 100 + S)
+    _check("f16", out, exp)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "q8"])
+def test_prefill_large_grid_d128(dev, dtype):
+    """More (query block, kv head) items than two a CU: the grid runs heaviest first instead of
+    in mirror pairs. Rows are independent, so a spread sample is checked."""
+    H, KV, D, S = 32, 8, 128, 4160
+    rng = np.random.default_rng(51)
+    k = rng.standard_normal((S, KV, D)).astype(np.float32)
+    v = rng.standard_normal((S, KV, D)).astype(np.float32)
+    q = rng.standard_normal((S, H, D)).astype(np.float32)
+    c = E.KvCache(1, KV, D, dtype, max_seq_len=S, capacity=S)
+    fill_cache_raw(c, 0, k, v)
+    out = run_attention(c, 0, q, 0)
+    kk, vv = cached_values(c, 0, 0, S)
+    for r0 in (0, 2000, S - 48):
+        rows = slice(r0, r0 + 48)
+        _check(dtype, out[rows], ref.attention(q[rows], kk[:r0 + 48], vv[:r0 + 48], r0))
+    c.close()
+
+
 @pytest.mark.parametrize("dtype", ["f16", "q8"])
 def test_prefill_hybrid_gate_d256(dev, dtype):
     out, exp = _raw_case(dtype, 24, 4, 256, 333, 333, seed=8, gate=True, scale=1.0 / 16)
