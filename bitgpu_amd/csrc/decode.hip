@@ -819,9 +819,9 @@ static int nset_for(int R) { return (R + 15) / 16; }
 
 // dynamic LDS of the tile loop and wave combine (DecodeSmem::total for the launch's template
 // arguments); the split merge needs less (weights and 16 float4 per split group)
-static size_t decode_lds_bytes(int D, int dtype, int R) {
+// NW: waves per workgroup (the most a shape launches with, 8 for D=128 single-set, bounds the rest)
+static size_t decode_lds_bytes(int D, int dtype, int R, int NW) {
   const int nset = nset_for(R);
-  const int NW = (D == 128 && nset == 1) ? 8 : 4;
   const int RS = 16 * nset, NT = D / 32, NBV = dtype == KV_Q8 ? D / 32 : 1;
   const size_t a = (size_t)((R + 3) / 4) * NT * 2 * 64 * 16 + 32 + (size_t)NW * ((size_t)NBV * RS * 32 * 2 + (size_t)RS * 4);
   const size_t b = (size_t)NW * R * (D + 5) * 4;
@@ -835,11 +835,9 @@ bool decode_supported(const LayerView& L, int S, int H) {
   const int G = H / L.kv_heads;
   const int R = G * S;
   // more rows than the operand and P^T tiles fit in LDS (D=256: about 20) go to the prefill kernel
-  return R >= 1 && nset_for(R) <= 3 && decode_lds_bytes(L.D, L.dtype, R) <= kDecodeLdsMax;
+  const int nw_max = (L.D == 128 && nset_for(R) == 1) ? 8 : 4;
+  return R >= 1 && nset_for(R) <= 3 && decode_lds_bytes(L.D, L.dtype, R, nw_max) <= kDecodeLdsMax;
 }
-
-// waves per workgroup: 8 where the registers allow two workgroups' worth per CU, else 4
-static int waves_for(int D, int nset) { return (D == 128 && nset == 1) ? 8 : 4; }
 
 struct Split { int n_tiles, tps, n_splits, n_scan, phys_limit; };
 
@@ -873,9 +871,8 @@ size_t decode_workspace_floats(const LayerView& L, int S, int H, int num_cus, si
   return (size_t)L.kv_heads * R * (L.D / 64) * ns_max * kUnitF4 * 4;
 }
 
-template <int D, int DT, bool ROLL, int NSET, int NPT>
+template <int D, int DT, bool ROLL, int NSET, int NPT, int NW>
 static hipError_t launch_cfg(const LayerView& L, const AttnArgs& a, hipStream_t st) {
-  constexpr int NW = (D == 128 && NSET == 1) ? 8 : 4;
   using SM = DecodeSmem<D, DT, ROLL, NSET, NW>;
   const Split sp = plan_split(L, a.S, a.pos_base, a.num_cus, NW);
   DecodeParams p;
@@ -902,7 +899,7 @@ static hipError_t launch_cfg(const LayerView& L, const AttnArgs& a, hipStream_t 
   p.n_mergers = units < sp.n_splits ? units : sp.n_splits;
   const int NP = (p.R + 3) / 4;
   size_t smem = SM::total(NP, p.R);
-  if (smem != decode_lds_bytes(D, DT, p.R)) return hipErrorInvalidValue;  // the two plans agree
+  if (smem != decode_lds_bytes(D, DT, p.R, NW)) return hipErrorInvalidValue;  // the two plans agree
   if (sp.n_splits > 1) {
     // the merge reuses the space: weights [NS] (16-byte aligned) and [waves][16] float4
     const size_t merge = (((size_t)sp.n_splits * 4 + 15) & ~(size_t)15) + (size_t)NW * 16 * 16;
@@ -926,13 +923,24 @@ template <int D, int DT, bool ROLL>
 static hipError_t launch_nset(const LayerView& L, const AttnArgs& a, int nset, hipStream_t st) {
   const int np = ((a.H / L.kv_heads) * a.S + 3) / 4;  // passes of 4 query rows
   switch (nset) {
-    case 1:
-      // decode shapes (G = 4 or 6 rows) get straight-line passes
-      if (np == 1) return launch_cfg<D, DT, ROLL, 1, 1>(L, a, st);
-      if (np == 2) return launch_cfg<D, DT, ROLL, 1, 2>(L, a, st);
-      return launch_cfg<D, DT, ROLL, 1, 0>(L, a, st);
-    case 2: return launch_cfg<D, DT, ROLL, 2, 0>(L, a, st);
-    default: return launch_cfg<D, DT, ROLL, 3, 0>(L, a, st);
+    case 1: {
+      // decode shapes (G = 4 or 6 rows) get straight-line passes. D=128 runs 8-wave workgroups
+      // (every wave takes at least one tile) when each CU gets 8 tiles or more; a shorter range
+      // runs 4-wave workgroups, which split it over twice as many CUs
+      const int n_scan = (L.ring.roll && L.ring.head != 0) ? L.max_seq : a.pos_base + a.S;
+      const long tiles = (long)(n_scan + 31) / 32 * L.kv_heads;
+      const int cus = a.num_cus > 0 ? a.num_cus : 256;
+      if (D == 128 && tiles >= 8L * cus) {
+        if (np == 1) return launch_cfg<D, DT, ROLL, 1, 1, 8>(L, a, st);
+        if (np == 2) return launch_cfg<D, DT, ROLL, 1, 2, 8>(L, a, st);
+        return launch_cfg<D, DT, ROLL, 1, 0, 8>(L, a, st);
+      }
+      if (np == 1) return launch_cfg<D, DT, ROLL, 1, 1, 4>(L, a, st);
+      if (np == 2) return launch_cfg<D, DT, ROLL, 1, 2, 4>(L, a, st);
+      return launch_cfg<D, DT, ROLL, 1, 0, 4>(L, a, st);
+    }
+    case 2: return launch_cfg<D, DT, ROLL, 2, 0, 4>(L, a, st);
+    default: return launch_cfg<D, DT, ROLL, 3, 0, 4>(L, a, st);
   }
 }
 
