@@ -939,7 +939,10 @@ static hipError_t launch_nset(const LayerView& L, const AttnArgs& a, int nset, h
       if (np == 2) return launch_cfg<D, DT, ROLL, 1, 2, 4>(L, a, st);
       return launch_cfg<D, DT, ROLL, 1, 0, 4>(L, a, st);
     }
-    case 2: return launch_cfg<D, DT, ROLL, 2, 0, 4>(L, a, st);
+    case 2:
+      // the 5-row verify of G = 4 heads (20 rows) gets its exact pass count
+      if (np == 5) return launch_cfg<D, DT, ROLL, 2, 5, 4>(L, a, st);
+      return launch_cfg<D, DT, ROLL, 2, 0, 4>(L, a, st);
     default: return launch_cfg<D, DT, ROLL, 3, 0, 4>(L, a, st);
   }
 }
