@@ -930,10 +930,12 @@ static hipError_t launch_nset(const LayerView& L, const AttnArgs& a, int nset, h
       const int n_scan = (L.ring.roll && L.ring.head != 0) ? L.max_seq : a.pos_base + a.S;
       const long tiles = (long)(n_scan + 31) / 32 * L.kv_heads;
       const int cus = a.num_cus > 0 ? a.num_cus : 256;
-      if (D == 128 && tiles >= 8L * cus) {
-        if (np == 1) return launch_cfg<D, DT, ROLL, 1, 1, 8>(L, a, st);
-        if (np == 2) return launch_cfg<D, DT, ROLL, 1, 2, 8>(L, a, st);
-        return launch_cfg<D, DT, ROLL, 1, 0, 8>(L, a, st);
+      if constexpr (D == 128) {
+        if (tiles >= 8L * cus) {
+          if (np == 1) return launch_cfg<D, DT, ROLL, 1, 1, 8>(L, a, st);
+          if (np == 2) return launch_cfg<D, DT, ROLL, 1, 2, 8>(L, a, st);
+          return launch_cfg<D, DT, ROLL, 1, 0, 8>(L, a, st);
+        }
       }
       if (np == 1) return launch_cfg<D, DT, ROLL, 1, 1, 4>(L, a, st);
       if (np == 2) return launch_cfg<D, DT, ROLL, 1, 2, 4>(L, a, st);
