@@ -420,18 +420,7 @@ __global__ __launch_bounds__(256, D == 128 ? 2 : 1) void prefill_kernel(PrefillP
 #pragma unroll
         for (int u = 0; u < NSUB; u++) ka[c][u].u = ldv(kc + k_chunk_pos<D>(u * 32 + n, 2 * c + g2) * 8);
       };
-      // P of group g = (u, t): 8 exp2 of x, f16, row sum
       const half2p ones = {(_Float16)1.0f, (_Float16)1.0f};
-      auto pgroup = [&](int g) {
-        const int u = g >> 1, t = g & 1;
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          pb[u][t].e[e] = (_Float16)__builtin_amdgcn_exp2f(x[u][8 * t + e] - m);
-          pb[u][t].e[4 + e] = (_Float16)__builtin_amdgcn_exp2f(x[u][8 * t + 4 + e] - m);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; i++) lsum = __builtin_amdgcn_fdot2(pb[u][t].p[i], ones, lsum, false);
-      };
       // in program order, each piece fenced: the reads of chunk c+2 ahead of chunk c's MFMAs,
       // then a share of the P work (the scheduler left alone runs one accumulator chain first
       // and waits for every read)
@@ -446,15 +435,17 @@ __global__ __launch_bounds__(256, D == 128 ? 2 : 1) void prefill_kernel(PrefillP
           sacc[acc] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[c][u].h, qf[c], sacc[acc], 0, 0, 0);
         }
         if constexpr (WP) {
-          // 2*NSUB groups of P over NC chunks
-          constexpr int GPC = (2 * NSUB + NC - 1) / NC;  // groups per chunk (>= 1)
-          constexpr int EVERY = NC / (2 * NSUB);         // chunks per group when fewer groups
-          if constexpr (EVERY >= 1) {
-            if (c % EVERY == EVERY - 1 && c / EVERY < 2 * NSUB) pgroup(c / EVERY);
-          } else {
+          // the 16*NSUB values of P spread evenly over the NC chunks, in order (so the row sum
+          // adds the same pairs in the same order as a whole group at a time would)
+          constexpr int NPI = 16 * NSUB, PER = (NPI + NC - 1) / NC;
 #pragma unroll
-            for (int k = 0; k < GPC; k++)
-              if (c * GPC + k < 2 * NSUB) pgroup(c * GPC + k);
+          for (int k = 0; k < PER; k++) {
+            const int i = c * PER + k;
+            if (i < NPI) {
+              const int u = i >> 4, e = i & 15;
+              pb[u][e >> 3].e[e & 7] = (_Float16)__builtin_amdgcn_exp2f(x[u][e] - m);
+              if (e & 1) lsum = __builtin_amdgcn_fdot2(pb[u][e >> 3].p[(e & 7) >> 1], ones, lsum, false);
+            }
           }
         }
         __builtin_amdgcn_sched_barrier(0);
