@@ -52,6 +52,7 @@ SIGNATURES = [
     ("bg_kv_evict", _i32, [_vp, _i32, _i32, _pi32]),
     ("bg_kv_evict_for", _i32, [_vp, _i32, _i32, _pi32]),
     ("bg_kv_ring_state", _i32, [_vp, _pi32, C.POINTER(C.c_int64)]),
+    ("bg_kv_ring_reset", _i32, [_vp, C.c_int64]),
     ("bg_kv_region_bytes", _i32, [_vp, _i32, _i32, C.POINTER(C.c_size_t)]),
     ("bg_kv_export_rows", _i32, [_vp, _i32, _i32, _i32, _i32, _vp, _vp]),
     ("bg_kv_import_rows", _i32, [_vp, _i32, _i32, _i32, _i32, _vp, _vp]),

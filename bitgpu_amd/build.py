@@ -1,6 +1,7 @@
 """Build the gfx950 HIP library ``bitgpu_amd/lib/libbitgpu_attn.so`` in-tree with hipcc.
 
-Usage: ``python -m bitgpu_amd.build`` (also called by ``__graft_entry__.build()``).
+Usage: ``python -m bitgpu_amd.build [--incremental]`` (also called by ``__graft_entry__.build()``,
+which always compiles everything).
 Every .hip file under csrc/ is compiled for gfx950 and linked into one shared library that
 exports the C ABI of include/bitgpu_attn.h.
 """
@@ -28,8 +29,16 @@ FLAGS = [
 ]
 
 
-def _compile(src: str) -> str:
+def _headers_mtime() -> float:
+    hs = [os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".h")]
+    hs.append(os.path.join(HERE, "..", "include", "bitgpu_attn.h"))
+    return max(os.path.getmtime(h) for h in hs if os.path.exists(h))
+
+
+def _compile(src: str, incremental: bool = False) -> str:
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
+    if incremental and os.path.exists(obj) and os.path.getmtime(obj) > max(os.path.getmtime(src), _headers_mtime()):
+        return obj
     cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
@@ -37,12 +46,14 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(verbose: bool = True) -> str:
+def build(verbose: bool = True, incremental: bool = False) -> str:
+    """Compile every csrc/*.hip for gfx950 and link the library (``incremental`` skips sources
+    whose object is newer than the source and every header: a development shortcut)."""
     os.makedirs(BUILD, exist_ok=True)
     os.makedirs(os.path.dirname(LIB), exist_ok=True)
     srcs = sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
     with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
-        objs = list(ex.map(_compile, srcs))
+        objs = list(ex.map(lambda f: _compile(f, incremental), srcs))
     tmp = LIB + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -75,7 +86,7 @@ def build_node_addon(verbose: bool = True) -> str | None:
 
 if __name__ == "__main__":
     try:
-        build()
+        build(incremental="--incremental" in sys.argv)
     except RuntimeError as e:
         print(e, file=sys.stderr)
         sys.exit(1)

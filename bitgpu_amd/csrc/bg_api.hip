@@ -608,6 +608,15 @@ int32_t bg_kv_ring_state(const bg_kv_cache* c, int32_t* head, int64_t* evicted) 
   return BG_OK;
 }
 
+int32_t bg_kv_ring_reset(bg_kv_cache* c, int64_t evicted) {
+  if (!c) return fail(BG_E_INVALID, "bg_kv_ring_reset: NULL cache");
+  if (!c->roll) return fail(BG_E_STATE, "bg_kv_ring_reset: cache is not in sink mode");
+  if (evicted < 0) return fail(BG_E_INVALID, "bg_kv_ring_reset: evicted %lld < 0", (long long)evicted);
+  c->head = 0;
+  c->evicted = evicted;
+  return BG_OK;
+}
+
 int32_t bg_kv_region_bytes(const bg_kv_cache* c, int32_t region, int32_t count, size_t* bytes) {
   if (!c || !bytes || count < 0) return fail(BG_E_INVALID, "bg_kv_region_bytes: bad arguments");
   if (region == BG_K || region == BG_V) {

@@ -9,6 +9,7 @@ The reference (stfurkan/bitgpu v0.19.1, src/engine.ts) records, per layer:
 * the full-attention branch of ``hybridLayer()`` (1465-1493)   -> :func:`hybrid_full_attention`
 * ``ensureKvCapacity`` / ``evict`` / ``evictFor`` / ``saveCache`` / ``restoreCache``
                                                                -> :class:`KvCache` methods
+  (restoreCache's checks, 2808-2845                           -> :func:`validate_snapshot`)
 * ``synthRope`` (117-147)                                      -> :func:`rope_tables`
 
 Device memory is owned by torch tensors (``cuda`` device, float32, contiguous); only raw
@@ -22,11 +23,11 @@ import math
 
 import numpy as np
 
-from ._lib import (BG_K, BG_KSCALE, BG_ROPE_ABSOLUTE, BG_ROPE_SLOT, BG_V, BG_VSCALE, KV_DTYPES, check,
-                   lib)
+from ._lib import (BG_E_INVALID, BG_E_STATE, BG_K, BG_KSCALE, BG_ROPE_ABSOLUTE, BG_ROPE_SLOT, BG_V, BG_VSCALE,
+                   KV_DTYPES, BitgpuError, check, lib)
 
 __all__ = ["KvCache", "attention", "qkv_prologue", "layer_attention", "hybrid_full_attention",
-           "rope_tables", "evict_plan", "ring_map"]
+           "rope_tables", "evict_plan", "ring_map", "validate_snapshot"]
 
 
 def _stream():
@@ -189,6 +190,58 @@ class KvCache:
         count = length - base
         return b"".join(self.export_rows(li, r, base, count) for li in range(self.n_layers) for r in self._regions())
 
+    def ring_reset(self, evicted: int = 0):
+        """Compacted ring state (origin 0): a new conversation, or the target of a v2 restore."""
+        check(lib().bg_kv_ring_reset(self._h, int(evicted)))
+
+    def model_stamp(self, hidden: int = 0, vocab: int = 0) -> dict:
+        """The KvSnapshot.model stamp (src/types.ts:377-378); hidden/vocab are the engine's."""
+        return {"layers": self.n_layers, "kvHeads": self.kv_heads, "headDim": self.head_dim, "hidden": hidden,
+                "vocab": vocab}
+
+    def save_cache(self, ids, cache_len: int | None = None, model: dict | None = None, base: int = 0):
+        """saveCache (src/engine.ts:2736-2805) over this cache: a KvSnapshot dict (src/types.ts:369-390).
+
+        ``ids`` is the conversation's fullHistory; the stored length is ``cache_len`` in sink
+        mode (slots, not history) and ``len(ids) - 1`` otherwise. Returns None for no history.
+        A sink-mode snapshot also records the rows evicted so far (``roll.evicted``, an extra
+        field the reference does not read) so an absolute-position cache restores exactly."""
+        if not ids:
+            return None
+        if self.roll:
+            if cache_len is None:
+                raise ValueError("saveCache: a sink-mode cache needs cache_len (its filled slots)")
+            length = int(cache_len)
+        else:
+            length = len(ids) - 1
+        base = max(0, min(int(base), length))
+        if base > 0 and self.roll:
+            raise BitgpuError(BG_E_STATE, "saveCache: delta snapshots ({ from }) are not supported under overflow 'sinks'")
+        snap = {"version": 2 if self.roll else 1, "kvCache": self.kv_cache,
+                "model": dict(model) if model else self.model_stamp(), "ids": list(ids),
+                "data": self.save_snapshot(length, base)}
+        if base > 0:
+            snap["base"] = base
+        if self.roll:
+            snap["roll"] = {"sinkTokens": self.sinks, "cacheLen": length, "evicted": self.ring_state()[1]}
+        return snap
+
+    def restore_cache(self, snap: dict, model: dict | None = None, cache_len: int = 0, history=()) -> int:
+        """restoreCache (src/engine.ts:2807-2872): validate ``snap`` against this cache (same
+        rejections and messages as the reference), then write its positions. ``cache_len`` and
+        ``history`` are the engine's current cacheLen / fullHistory (a delta restore must sit
+        exactly on its prefix). Returns the restored cacheLen. A v2 snapshot restores into the
+        compacted ring (origin 0), the reference's layout after any eviction."""
+        length, base, count = validate_snapshot(
+            snap, roll=self.roll, sinks=self.sinks, kv_cache=self.kv_cache,
+            model=dict(model) if model else self.model_stamp(), max_seq_len=self.max_seq_len,
+            data_bytes=self.n_layers * sum(self.region_bytes(r, 1) for r in self._regions()),
+            cache_len=cache_len, history=history)
+        if self.roll:
+            self.ring_reset(int(snap["roll"].get("evicted", 0)))
+        self.restore_snapshot(snap["data"], length, base)
+        return length
+
     def restore_snapshot(self, data: bytes, length: int, base: int = 0):
         """KV part of restoreCache (src/engine.ts:2807-2872)."""
         count = length - base
@@ -202,6 +255,51 @@ class KvCache:
                 n = self.region_bytes(r, count)
                 self.import_rows(li, r, base, count, data[off: off + n])
                 off += n
+
+
+def validate_snapshot(snap, *, roll: bool, sinks: int, kv_cache: str, model: dict, max_seq_len: int,
+                      data_bytes: int, cache_len: int = 0, history=()):
+    """The checks of restoreCache (src/engine.ts:2808-2845), host-only, in the reference's order
+    and wording. ``data_bytes`` is snapshotBytes(1) (per-position bytes over every layer).
+    Raises BitgpuError; returns (len, base, count)."""
+    def bad(msg):
+        raise BitgpuError(BG_E_INVALID, msg)
+    if not snap or snap.get("version") not in (1, 2):
+        bad(f"restoreCache: unsupported snapshot version {snap.get('version') if snap else None}")
+    v2 = snap["version"] == 2
+    if v2 != bool(roll):
+        bad("restoreCache: snapshot was saved under overflow 'sinks' (unroped keys); this engine runs overflow 'error'"
+            if v2 else
+            "restoreCache: snapshot was saved under overflow 'error' (roped keys); this engine runs overflow 'sinks'")
+    rollinfo = snap.get("roll") or {}
+    if v2 and rollinfo.get("sinkTokens") != sinks:
+        bad(f"restoreCache: snapshot uses {rollinfo.get('sinkTokens')} sink tokens but this engine uses {sinks}")
+    if snap.get("kvCache") != kv_cache:
+        bad(f"restoreCache: snapshot was saved under kvCache '{snap.get('kvCache')}' but this engine runs "
+            f"'{kv_cache}' - snapshots do not convert across modes")
+    m = snap.get("model")
+    keys = ("layers", "kvHeads", "headDim", "hidden", "vocab")
+    if not m or any(m.get(k) != model.get(k) for k in keys):
+        bad("restoreCache: snapshot is from a different model (architecture mismatch)")
+    ids = snap.get("ids")
+    if not isinstance(ids, (list, tuple)) or len(ids) == 0:
+        bad("restoreCache: snapshot holds no tokens")
+    length = int(rollinfo["cacheLen"]) if v2 else len(ids) - 1
+    base = max(0, int(math.floor(snap.get("base") or 0)))
+    count = length - base
+    need = length + (0 if v2 else 1)
+    if need > max_seq_len:
+        bad(f"restoreCache: snapshot needs {need} cache slots but maxSeqLen is {max_seq_len}")
+    if len(snap["data"]) != data_bytes * count:
+        bad(f"restoreCache: snapshot data is {len(snap['data'])} bytes, expected {data_bytes * count}")
+    if base > 0:
+        if cache_len != base:
+            bad(f"restoreCache: delta snapshot expects the cache at position {base} (prewarm the shared prefix "
+                f"first); it is at {cache_len}")
+        for i in range(base):
+            if i >= len(history) or history[i] != ids[i]:
+                bad(f"restoreCache: delta snapshot prefix does not match the current prewarm (token {i})")
+    return length, base, count
 
 
 def attention(cache: KvCache, li: int, qr, S: int, H: int, pos_base: int, scale: float | None = None,

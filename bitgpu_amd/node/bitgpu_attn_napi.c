@@ -240,6 +240,25 @@ static napi_value js_kv_evict_for(napi_env env, napi_callback_info info) {
   return i32(env, nf);
 }
 
+/* kvRingState(cache) -> [head, evicted]; kvRingReset(cache, evicted) */
+static napi_value js_kv_ring_state(napi_env env, napi_callback_info info) {
+  ARGS(1);
+  int32_t head;
+  int64_t ev;
+  RC(bg_kv_ring_state(arg_cache(env, a[0]), &head, &ev));
+  napi_value r, x;
+  napi_create_array_with_length(env, 2, &r);
+  napi_set_element(env, r, 0, i32(env, head));
+  napi_create_double(env, (double)ev, &x);
+  napi_set_element(env, r, 1, x);
+  return r;
+}
+static napi_value js_kv_ring_reset(napi_env env, napi_callback_info info) {
+  ARGS(2);
+  RC(bg_kv_ring_reset(arg_cache(env, a[0]), (int64_t)arg_f64(env, a[1])));
+  return NULL;
+}
+
 static napi_value js_kv_region_bytes(napi_env env, napi_callback_info info) {
   ARGS(3);
   size_t b;
@@ -357,6 +376,8 @@ static napi_value init(napi_env env, napi_value exports) {
       {"attention", 0, js_attention, 0, 0, 0, napi_default, 0},
       {"kvEvict", 0, js_kv_evict, 0, 0, 0, napi_default, 0},
       {"kvEvictFor", 0, js_kv_evict_for, 0, 0, 0, napi_default, 0},
+      {"kvRingState", 0, js_kv_ring_state, 0, 0, 0, napi_default, 0},
+      {"kvRingReset", 0, js_kv_ring_reset, 0, 0, 0, napi_default, 0},
       {"kvRegionBytes", 0, js_kv_region_bytes, 0, 0, 0, napi_default, 0},
       {"kvExportRows", 0, js_kv_export, 0, 0, 0, napi_default, 0},
       {"kvImportRows", 0, js_kv_import, 0, 0, 0, napi_default, 0},

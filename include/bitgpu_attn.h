@@ -169,6 +169,13 @@ int32_t bg_kv_evict_for(bg_kv_cache* cache, int32_t fill, int32_t n, int32_t* ne
  * L >= sinks is L + evicted). */
 int32_t bg_kv_ring_state(const bg_kv_cache* cache, int32_t* head, int64_t* evicted);
 
+/* Put the sink-mode ring into its compacted state: origin 0, `evicted` rows evicted before
+ * logical slot `sinks` (0 for a new conversation). The reference's cache is always compacted
+ * (evict() moves the kept rows to slot `sinks`, src/engine.ts:1206-1209), so a v2 snapshot
+ * restore (restoreCache, src/engine.ts:2807-2872) writes logical slots 0..cacheLen-1 into this
+ * state, and a fresh conversation (cacheLen = 0) starts from it. Contents are not touched. */
+int32_t bg_kv_ring_reset(bg_kv_cache* cache, int64_t evicted);
+
 /* ---- snapshot wire format -----------------------------------------------------------------
  * Per-region export/import in the reference snapshot layout (src/engine.ts:2724-2734,
  * 2757-2771, 2847-2860): region BG_K / BG_V is [count, KV, head_dim] elements of the storage

@@ -16,10 +16,13 @@ Pinning (what fixes each function independently of its own formula; tests/test_o
   frequency closed form, the reference's own rope_partial case tables.
 * ``rmsnorm`` / ``rmsnorm_gemma`` -- constant-row closed form, float64 recomputation,
   scale invariance.
-* ``rope_apply`` -- position 0 is the identity, pair norms are preserved, relative-position
-  property of the rotated dot product, passthrough of dims >= rot.
+* ``rope_apply`` -- the rotation direction by the unit-vector closed form (e_j -> (cos, +sin),
+  e_{j+h} -> (-sin, cos)) and by Python complex multiplication, position 0 is the identity,
+  pair norms are preserved, relative-position property, passthrough of dims >= rot.
 * ``attention`` -- explicit float64 loop with ``math.exp`` on tiny shapes, rows of P sum to 1,
   uniform V, one dominant key, single key, GQA grouping by explicit per-head loop.
+* ``sigmoid`` / ``gated_attention`` -- sigma(0) = 1/2, sigma(x) + sigma(-x) = 1, Python
+  ``1/(1+math.exp(-x))``, saturation; the gated composite against an f64 ``math.exp`` loop.
 * ``q8_pack`` / ``q8_dequant`` -- zero block, block maximum -> +-127, negative zero, exact
   tie (WGSL ``floor(0.5 + 127 e)``, not round-to-even), exhaustive small grid against exact
   rational arithmetic, and the independent C restatement ``oracle/pack_ref.c``.

@@ -190,3 +190,63 @@ def test_stream_and_event_utilities(dev):
         _lib.check(lib.bg_event_destroy(ev))
     _lib.check(lib.bg_stream_destroy(st))
     c.close()
+
+
+@pytest.mark.parametrize("dtype", ["f16", "q8", "f32"])
+def test_v2_snapshot_restores_into_a_wrapped_ring(dev, dtype):
+    """saveCache / restoreCache under overflow 'sinks' (src/engine.ts:2736-2872): a v2 snapshot
+    of a cache whose ring has wrapped restores into another sink-mode cache whose ring origin is
+    elsewhere; the restored logical slots hold the same bytes and attention over them matches
+    the oracle (keys rotated at read by their slot). Restoring it into an overflow 'error'
+    cache is rejected with the reference's message."""
+    rng = np.random.default_rng(61)
+    H, KV, D, sinks, max_seq = 32, 8, 128, 4, 260
+    from tests.gpu_helpers import rope_dev
+    cos_d, sin_d, cos, sin = rope_dev(1e6, D, max_seq)
+
+    def sink_cache():
+        c = E.KvCache(1, KV, D, dtype, max_seq_len=max_seq, overflow="sinks", sink_tokens=sinks)
+        c.set_rope(cos_d, sin_d)
+        return c
+
+    a = sink_cache()
+    k0 = rng.standard_normal((200, KV, D)).astype(np.float32)
+    fill_cache_raw(a, 0, k0, k0[::-1].copy())
+    fill = a.evict_for(200, 100)                       # evict(200, 40): drops a 64-row batch
+    assert fill == ref.evict(200, 40, sinks, max_seq)[0] == 136
+    k1 = rng.standard_normal((100, KV, D)).astype(np.float32)
+    v1 = rng.standard_normal((100, KV, D)).astype(np.float32)
+    fill_cache_raw(a, 0, k1, v1, row0=fill)
+    n = fill + 100
+    assert a.ring_state()[0] != 0
+    snap = a.save_cache(ids=list(range(1000)), cache_len=n)
+    assert snap["version"] == 2 and snap["roll"]["cacheLen"] == n and snap["roll"]["sinkTokens"] == sinks
+
+    b = sink_cache()
+    junk = rng.standard_normal((max_seq, KV, D)).astype(np.float32)
+    fill_cache_raw(b, 0, junk, junk)
+    assert b.evict_for(max_seq, 10) == 196             # origin 64
+    assert b.evict_for(196, 70) == 132                 # a second batch of 64: origin 128
+    assert b.ring_state()[0] not in (0, a.ring_state()[0])
+    assert b.restore_cache(snap) == n
+    assert b.ring_state() == (0, a.ring_state()[1])
+    for x, y in zip(export_k_v(a, 0, 0, n), export_k_v(b, 0, 0, n)):
+        if x is not None:
+            assert np.array_equal(x, y)
+    q = rng.standard_normal((1, H, D)).astype(np.float32)
+    kst, vst, ks, vs = export_k_v(b, 0, 0, n)
+    if dtype == "q8":
+        kst, vst = ref.q8_dequant(kst, ks), ref.q8_dequant(vst, vs)
+    kk = ref.rope_apply(kst.astype(np.float32), cos, sin, np.arange(n))
+    exp = ref.attention(q, kk, vst.astype(np.float32), n - 1)
+    for c in (a, b):
+        out = run_attention(c, 0, q, n - 1)
+        if dtype == "f32":
+            assert np.abs(out - exp).max() <= 1e-4
+        else:
+            assert np.abs(out - exp).max() / np.abs(exp).max() <= 2e-3
+    plain = E.KvCache(1, KV, D, dtype, max_seq_len=max_seq)
+    with pytest.raises(BitgpuError, match="saved under overflow 'sinks'"):
+        plain.restore_cache(snap)
+    for c in (a, b, plain):
+        c.close()

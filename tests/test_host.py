@@ -120,3 +120,52 @@ def test_ring_map_is_a_permutation():
     for head in (0, 1, 17, 4095):
         p = [E.ring_map(4, 4100, head, L) for L in range(4100)]
         assert sorted(p) == list(range(4100)) and p[:4] == [0, 1, 2, 3]
+
+
+# ---------------------------------------------------------------- restoreCache checks
+def _snap(**kw):
+    s = {"version": 2, "kvCache": "f16", "model": {"layers": 2, "kvHeads": 8, "headDim": 128, "hidden": 0, "vocab": 0},
+         "ids": list(range(50)), "roll": {"sinkTokens": 4, "cacheLen": 40}, "data": b"\0" * (40 * 100)}
+    s.update(kw)
+    return s
+
+
+_MODEL = {"layers": 2, "kvHeads": 8, "headDim": 128, "hidden": 0, "vocab": 0}
+
+
+def _validate(snap, roll=True, sinks=4, kv="f16", model=_MODEL, max_seq=4100, cache_len=0, history=()):
+    return E.validate_snapshot(snap, roll=roll, sinks=sinks, kv_cache=kv, model=model, max_seq_len=max_seq,
+                               data_bytes=100, cache_len=cache_len, history=history)
+
+
+@pytest.mark.parametrize("snap,kw,msg", [
+    (_snap(version=3), {}, "unsupported snapshot version 3"),
+    (_snap(), {"roll": False}, "saved under overflow 'sinks'"),
+    (_snap(version=1, roll=None, data=b"\0" * 4900), {}, "saved under overflow 'error'"),
+    (_snap(roll={"sinkTokens": 2, "cacheLen": 40}), {}, "uses 2 sink tokens but this engine uses 4"),
+    (_snap(kvCache="q8"), {}, "kvCache 'q8' but this engine runs 'f16'"),
+    (_snap(), {"model": dict(_MODEL, headDim=256)}, "different model"),
+    (_snap(ids=[]), {}, "holds no tokens"),
+    (_snap(roll={"sinkTokens": 4, "cacheLen": 5000}, data=b"\0" * 500000), {}, "needs 5000 cache slots"),
+    (_snap(data=b"\0" * 3999), {}, "expected 4000"),
+])
+def test_restore_rejections(snap, kw, msg):
+    """Every rejection of restoreCache (src/engine.ts:2808-2845), host-only."""
+    with pytest.raises(_lib.BitgpuError, match=msg):
+        _validate(snap, **kw)
+
+
+def test_restore_lengths_and_delta_prefix():
+    assert _validate(_snap()) == (40, 0, 40)                                  # v2: roll.cacheLen
+    v1 = _snap(version=1, roll=None, data=b"\0" * 4900)
+    assert _validate(v1, roll=False) == (49, 0, 49)                           # v1: ids.length - 1
+    # v2 may restore exactly full (cacheLen == maxSeqLen); v1 needs one spare slot
+    assert _validate(_snap(roll={"sinkTokens": 4, "cacheLen": 100}, data=b"\0" * 10000), max_seq=100)[0] == 100
+    with pytest.raises(_lib.BitgpuError, match="needs 50 cache slots but maxSeqLen is 49"):
+        _validate(v1, roll=False, max_seq=49)
+    d = _snap(version=1, roll=None, base=10, data=b"\0" * 3900)
+    assert _validate(d, roll=False, cache_len=10, history=list(range(10))) == (49, 10, 39)
+    with pytest.raises(_lib.BitgpuError, match="expects the cache at position 10"):
+        _validate(d, roll=False, cache_len=12, history=list(range(12)))
+    with pytest.raises(_lib.BitgpuError, match=r"prefix does not match the current prewarm \(token 3\)"):
+        _validate(d, roll=False, cache_len=10, history=[0, 1, 2, 7, 4, 5, 6, 7, 8, 9])

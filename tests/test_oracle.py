@@ -98,6 +98,38 @@ def test_rope_identity_norms_and_relative_position():
     assert abs(d1 - d2) < 1e-4
 
 
+def test_rope_direction_is_complex_multiplication():
+    """Unit-vector closed form: with z = x_j + i*x_{j+h}, RoPE is z * exp(i*p*inv_j), so e_j
+    goes to (cos, +sin) at dims (j, j+h) and e_{j+h} to (-sin, cos). A sign flip of the
+    rotate_half term (tools/reference.py:151-152) exchanges the two sines and fails here."""
+    theta, rot, D = 1e6, 128, 128
+    h = rot // 2
+    cos, sin = ref.rope_tables(theta, rot, 4000)
+    for p in (1, 17, 3999):
+        for j in (0, 5, h - 1):
+            a = p * (1.0 / math.pow(theta, 2 * j / rot))
+            c32, s32 = np.float32(math.cos(a)), np.float32(math.sin(a))
+            ej = np.zeros((1, 1, D), np.float32)
+            ej[0, 0, j] = 1
+            y = ref.rope_apply(ej, cos, sin, [p])[0, 0]
+            assert y[j] == c32 and y[j + h] == s32
+            assert np.count_nonzero(y) == 2
+            ejh = np.zeros((1, 1, D), np.float32)
+            ejh[0, 0, j + h] = 1
+            y = ref.rope_apply(ejh, cos, sin, [p])[0, 0]
+            assert y[j] == -s32 and y[j + h] == c32
+    # a general vector against Python complex arithmetic in f64 (partial rotation, rot = 64)
+    rng = np.random.default_rng(11)
+    cos, sin = ref.rope_tables(1e7, 64, 300)
+    x = rng.standard_normal((1, 1, 256)).astype(np.float32)
+    y = ref.rope_apply(x, cos, sin, [257], rot=64)[0, 0]
+    for j in range(32):
+        a = 257 * (1.0 / math.pow(1e7, 2 * j / 64))
+        z = complex(float(x[0, 0, j]), float(x[0, 0, j + 32])) * complex(math.cos(a), math.sin(a))
+        assert abs(y[j] - z.real) < 1e-6 and abs(y[j + 32] - z.imag) < 1e-6
+    assert np.array_equal(y[64:], x[0, 0, 64:])
+
+
 def test_rope_partial_passthrough_and_reference_case():
     from tests.golden.make_golden import reference_kernel_case_inputs
     g = np.load(os.path.join(ROOT, "tests", "golden", "ref_kernel_cases.npz"))
@@ -166,6 +198,41 @@ def test_attention_reference_kernel_case(cref):
     want = np.zeros_like(got)
     cref.oracle_attention_f64(_p(q), _p(k), _p(v), None, 6, 4, 2, 256, 6, 0, 1.0 / math.sqrt(256), _p(want))
     assert np.abs(got - want).max() < 1e-6
+
+
+def test_sigmoid_closed_forms():
+    """tools/qwen35_numpy.py:58-59 and gate_sigmoid.wgsl:13: sigma(0) = 1/2, sigma(x) +
+    sigma(-x) = 1, saturation, and agreement with Python's 1/(1+math.exp(-x))."""
+    x = np.array([0.0, 1.0, -1.0, 3.5, -7.25, 20.0, -20.0, 1e-4, 88.0, -88.0], np.float32)
+    s = ref.sigmoid(x)
+    assert s[0] == np.float32(0.5)
+    for xi, si in zip(x, s):
+        want = 1.0 / (1.0 + math.exp(-float(xi)))
+        assert abs(float(si) - want) <= 2 * float(np.spacing(np.float32(want)))
+    rng = np.random.default_rng(12)
+    r = (rng.standard_normal(1000) * 4).astype(np.float32)
+    assert np.allclose(ref.sigmoid(r) + ref.sigmoid(-r), 1.0, atol=1.2e-7)
+    assert ref.sigmoid(np.float32(-200)) == 0 and ref.sigmoid(np.float32(200)) == 1
+    assert np.all(np.diff(ref.sigmoid(np.sort(r))) >= 0)                     # monotone
+
+
+def test_gated_attention_bruteforce():
+    """Gated full attention (tools/qwen35_numpy.py:102-114) against an f64 loop with math.exp
+    for the softmax and for the gate 1/(1+exp(-g)); scale 1/sqrt(D) (qwen35_numpy.py:105)."""
+    rng = np.random.default_rng(13)
+    S, H, KV, D, pb = 3, 6, 2, 16, 5
+    q = rng.standard_normal((S, H, D)).astype(np.float32)
+    k = rng.standard_normal((pb + S, KV, D)).astype(np.float32)
+    v = rng.standard_normal((pb + S, KV, D)).astype(np.float32)
+    g = rng.standard_normal((S, H, D)).astype(np.float32) * 3
+    got = ref.gated_attention(q, k, v, g, pb)
+    att = _brute_attention(q, k, v, pb, 1 / math.sqrt(D))
+    gate = np.vectorize(lambda t: 1.0 / (1.0 + math.exp(-t)))(g.astype(np.float64))
+    assert np.allclose(got, att * gate, atol=2e-6)
+    # a gate of +inf-like size passes the attention through, a very negative one zeroes it
+    big = np.full_like(g, 100)
+    assert np.allclose(ref.gated_attention(q, k, v, big, pb), att, atol=2e-6)
+    assert np.all(ref.gated_attention(q, k, v, -big, pb) == 0)
 
 
 # ---------------------------------------------------------------- q8 quantizer
