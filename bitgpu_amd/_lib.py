@@ -33,6 +33,7 @@ SIGNATURES = [
     ("bg_evict_plan", _i32, [_i32, _i32, _i32, _i32, _pi32, _pi32, _pi32]),
     ("bg_ring_map", _i32, [_i32, _i32, _i32, _i32, _pi32]),
     ("bg_stream_sync", _i32, [_vp]),
+    ("bg_decode_plan", _i32, [_i32] * 8 + [_pi32]),
     ("bg_stream_create", _i32, [C.POINTER(_vp)]),
     ("bg_stream_destroy", _i32, [_vp]),
     ("bg_event_create", _i32, [C.POINTER(_vp)]),

@@ -8,6 +8,8 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
+#include <set>
 #include <string>
 #include <vector>
 
@@ -37,6 +39,13 @@ struct bg_kv_cache {
   void* pf16 = nullptr;
   int pf16_cap = 0;
   int num_cus = 256;
+  // decode merge error word: pinned, coherent host memory the kernel writes when a merger's
+  // bounded wait gives up (err_dev is its device address)
+  unsigned* err_host = nullptr;
+  unsigned* err_dev = nullptr;
+  // snapshot staging buffer (grown on demand, kept until destroy)
+  void* stage = nullptr;
+  size_t stage_bytes = 0;
 };
 
 namespace {
@@ -107,6 +116,43 @@ void free_layers(std::vector<void*>& k, std::vector<void*>& v, std::vector<float
 
 // slots the caller may address: the window in sink mode, the grown capacity otherwise
 int addressable(const bg_kv_cache* c) { return c->roll ? c->max_seq : c->capacity; }
+
+// live caches, for bg_stream_sync's check of their merge error words
+std::mutex g_caches_mu;
+std::set<bg_kv_cache*> g_caches;
+
+int env_int(const char* name, int dflt) {
+  const char* v = getenv(name);
+  return (v && *v) ? atoi(v) : dflt;
+}
+
+bool capturing(hipStream_t st) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  return cs != hipStreamCaptureStatusNone;
+}
+
+// An earlier decode launch on this cache gave up waiting for a split partial (its output was
+// stored as NaN): wait for every launch to finish, refill the split workspace with the empty
+// marker (a late partial may have landed after its merger gave up) and report it once.
+int32_t take_merge_error(bg_kv_cache* c, hipStream_t st) {
+  if (!c->err_host || __atomic_load_n(c->err_host, __ATOMIC_ACQUIRE) == 0) return BG_OK;
+  if (capturing(st))
+    return fail(BG_E_DEVICE, "an earlier decode split merge gave up waiting for a split; call bg_stream_sync "
+                             "outside graph capture to reset the workspace");
+  hipError_t e = hipDeviceSynchronize();
+  if (e == hipSuccess && c->ws)
+    e = hipMemsetD32((hipDeviceptr_t)c->ws, (int)bg::decode_workspace_empty(), c->ws_floats);
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e != hipSuccess) return hip_fail(e, "workspace reset after a merge timeout");
+  __atomic_store_n(c->err_host, 0u, __ATOMIC_RELEASE);
+  return fail(BG_E_DEVICE, "decode split merge gave up waiting for a split (GPU shared or oversubscribed): the "
+                           "outputs of bg_attention calls on this cache since the last check are NaN; the split "
+                           "workspace has been reset");
+}
 
 }  // namespace
 
@@ -180,7 +226,13 @@ int32_t bg_ring_map(int32_t sinks, int32_t max_seq_len, int32_t head, int32_t lo
 
 int32_t bg_stream_sync(void* stream) {
   hipError_t e = stream ? hipStreamSynchronize((hipStream_t)stream) : hipDeviceSynchronize();
-  return e == hipSuccess ? BG_OK : hip_fail(e, "stream sync");
+  if (e != hipSuccess) return hip_fail(e, "stream sync");
+  std::lock_guard<std::mutex> lock(g_caches_mu);
+  for (bg_kv_cache* c : g_caches) {
+    int32_t rc = take_merge_error(c, (hipStream_t)stream);
+    if (rc != BG_OK) return rc;
+  }
+  return BG_OK;
 }
 
 int32_t bg_stream_create(void** stream) {
@@ -292,13 +344,32 @@ int32_t bg_kv_create(int32_t n_layers, int32_t kv_heads, int32_t head_dim, int32
       return hip_fail(e, "KV cache allocation");
     }
   }
+  hipError_t e = hipHostMalloc((void**)&c->err_host, 64, hipHostMallocMapped | hipHostMallocCoherent);
+  if (e == hipSuccess) e = hipHostGetDevicePointer((void**)&c->err_dev, c->err_host, 0);
+  if (e != hipSuccess) {
+    if (c->err_host) (void)hipHostFree(c->err_host);
+    free_layers(c->k, c->v, c->ks, c->vs);
+    delete c;
+    return hip_fail(e, "KV cache error word allocation");
+  }
+  *c->err_host = 0;
+  {
+    std::lock_guard<std::mutex> lock(g_caches_mu);
+    g_caches.insert(c);
+  }
   *out = c;
   return BG_OK;
 }
 
 int32_t bg_kv_destroy(bg_kv_cache* c) {
   if (!c) return BG_OK;
+  {
+    std::lock_guard<std::mutex> lock(g_caches_mu);
+    g_caches.erase(c);
+  }
   (void)hipDeviceSynchronize();
+  if (c->err_host) (void)hipHostFree(c->err_host);
+  if (c->stage) (void)hipFree(c->stage);
   free_layers(c->k, c->v, c->ks, c->vs);
   if (c->ws) (void)hipFree(c->ws);
   if (c->ws_count) (void)hipFree(c->ws_count);
@@ -521,6 +592,9 @@ int32_t bg_attention(bg_kv_cache* c, int32_t layer, const float* q, int32_t S, i
     if (c->rope_positions < need)
       return fail(BG_E_INVALID, "bg_attention: rope table has %d rows, read-time rotation needs %ld", c->rope_positions, need);
   }
+  hipStream_t st = (hipStream_t)stream;
+  int32_t rc0 = take_merge_error(c, st);
+  if (rc0 != BG_OK) return rc0;
   LayerView L = view(c, layer);
   bg::AttnArgs a;
   a.q = q;
@@ -536,7 +610,11 @@ int32_t bg_attention(bg_kv_cache* c, int32_t layer, const float* q, int32_t S, i
   a.ws_count = nullptr;
   a.ws_floats = 0;
   a.num_cus = c->num_cus;
-  hipStream_t st = (hipStream_t)stream;
+  // test hooks (host-set): a tiny poll bound and a split that stores no partial make the merge
+  // give up while every kernel still exits normally
+  a.err = c->err_dev;
+  a.spin_limit = env_int("BG_DEBUG_MERGE_SPIN", 0);
+  a.withhold_split = env_int("BG_DEBUG_WITHHOLD_SPLIT", -1);
   hipError_t e;
   if (c->dtype == BG_KV_F32 && bg::f32_split_supported(L, S, H)) {
     int32_t rc = ensure_workspace(c, S, H);
@@ -608,6 +686,29 @@ int32_t bg_kv_ring_state(const bg_kv_cache* c, int32_t* head, int64_t* evicted) 
   return BG_OK;
 }
 
+int32_t bg_decode_plan(int32_t kv_heads, int32_t head_dim, int32_t dtype, int32_t S, int32_t H, int32_t pos_base,
+                       int32_t num_cus, int32_t resident_per_cu, int32_t* out) {
+  if (!out || kv_heads < 1 || S < 1 || H < kv_heads || H % kv_heads || pos_base < 0 || num_cus < 1 ||
+      resident_per_cu < 1 || (head_dim != 128 && head_dim != 256))
+    return fail(BG_E_INVALID, "bg_decode_plan: bad arguments");
+  LayerView L{};
+  L.kv_heads = kv_heads;
+  L.D = head_dim;
+  L.dtype = dtype;
+  L.cap = round32(pos_base + S);
+  L.max_seq = L.cap;
+  bg::DecodePlan p;
+  if (!bg::decode_plan(L, S, H, pos_base, num_cus, resident_per_cu, &p))
+    return fail(BG_E_UNSUPPORTED, "bg_decode_plan: the decode kernel does not take S %d, heads %d", S, H);
+  out[0] = p.waves;
+  out[1] = p.n_splits;
+  out[2] = p.tiles_per_split;
+  out[3] = p.n_mergers;
+  out[4] = p.grid;
+  out[5] = p.n_tiles;
+  return BG_OK;
+}
+
 int32_t bg_kv_ring_reset(bg_kv_cache* c, int64_t evicted) {
   if (!c) return fail(BG_E_INVALID, "bg_kv_ring_reset: NULL cache");
   if (!c->roll) return fail(BG_E_STATE, "bg_kv_ring_reset: cache is not in sink mode");
@@ -640,9 +741,18 @@ static int32_t transfer(bg_kv_cache* c, int32_t layer, int32_t region, int32_t b
     return fail(BG_E_INVALID, "snapshot transfer: positions %d..%d beyond capacity %d", base, base + count - 1, addressable(c));
   if (count == 0) return BG_OK;
   hipStream_t st = (hipStream_t)stream;
-  void* dev = nullptr;
-  hipError_t e = hipMalloc(&dev, bytes);
-  if (e != hipSuccess) return hip_fail(e, "snapshot staging allocation");
+  hipError_t e = hipSuccess;
+  if (bytes > c->stage_bytes) {
+    // wait for earlier transfers that use the old buffer, then grow it
+    e = hipDeviceSynchronize();
+    if (e == hipSuccess && c->stage) e = hipFree(c->stage);
+    c->stage = nullptr;
+    c->stage_bytes = 0;
+    if (e == hipSuccess) e = hipMalloc(&c->stage, bytes);
+    if (e != hipSuccess) return hip_fail(e, "snapshot staging allocation");
+    c->stage_bytes = bytes;
+  }
+  void* dev = c->stage;
   LayerView L = view(c, layer);
   if (import_) {
     e = hipMemcpyAsync(dev, host, bytes, hipMemcpyHostToDevice, st);
@@ -652,7 +762,6 @@ static int32_t transfer(bg_kv_cache* c, int32_t layer, int32_t region, int32_t b
     if (e == hipSuccess) e = hipMemcpyAsync(host, dev, bytes, hipMemcpyDeviceToHost, st);
   }
   if (e == hipSuccess) e = st ? hipStreamSynchronize(st) : hipDeviceSynchronize();
-  (void)hipFree(dev);
   return e == hipSuccess ? BG_OK : hip_fail(e, import_ ? "snapshot import" : "snapshot export");
 }
 

@@ -60,6 +60,9 @@ struct AttnArgs {
   // split-K workspace
   float* ws_o; float* ws_ml; unsigned* ws_count; size_t ws_floats;
   int num_cus;
+  // decode merge: host-visible error word, poll bound (0: default) and a test hook that makes
+  // one split store no partial (-1: none)
+  unsigned* err; int spin_limit; int withhold_split;
 };
 hipError_t launch_attention_f32(const LayerView& L, const AttnArgs& a, hipStream_t st);
 // split-K f32 decode / verify (G*S <= 16 rows per kv head), workspace as for the decode kernel
@@ -73,6 +76,14 @@ hipError_t launch_attention_prefill(const LayerView& L, const AttnArgs& a, hipSt
 size_t decode_workspace_floats(const LayerView& L, int S, int H, int num_cus, size_t* counters);
 uint32_t decode_workspace_empty();
 bool decode_supported(const LayerView& L, int S, int H);
+// the split-K plan of a decode launch (host-only arithmetic; false when the kernel does not take
+// the shape). resident_per_cu: workgroups of the launch's instantiation a CU holds at once.
+struct DecodePlan {
+  int waves, nset, passes;
+  int n_scan, phys_limit, n_tiles;
+  int tiles_per_split, n_splits, n_mergers, grid;
+};
+bool decode_plan(const LayerView& L, int S, int H, int pos_base, int num_cus, int resident_per_cu, DecodePlan* out);
 bool prefill_supported(const LayerView& L, int S, int H);
 // a q8 prefill of S rows that stages each K/V tile for enough query blocks to run faster on an
 // f16 copy of the attended slots

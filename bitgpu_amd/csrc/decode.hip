@@ -18,12 +18,20 @@
 //           through a 2 KB-per-block LDS transpose into the B operand of
 //   PV    = v_mfma_f32_16x16x32_f16 with V^T (the cache's transposed V tile, 16 B per lane)
 //           as A and P^T as B.
-//   merge = the waves combine through LDS; splits write (m, l, o) partials and a per-split
-//           flag stamped with the launch epoch; the first splits of each kv head poll the
-//           flags and each does the log-sum-exp merge, the output gate (gate_sigmoid.wgsl:13)
-//           and the store for its (row, 64-dim) units -- one launch per layer.
+//   merge = the waves combine through LDS; splits write (m, l, o) partials into slots that
+//           hold an "empty" marker between launches; the last splits of each kv head poll
+//           their units' slots and each does the log-sum-exp merge, the output gate
+//           (gate_sigmoid.wgsl:13) and the store for its (row, 64-dim) units -- one launch per
+//           layer. A merger waits only on splits dispatched before it, the grid never exceeds
+//           what the GPU holds at once, and the wait is bounded: a merger that gives up stores
+//           NaN and raises the cache's host-visible error word (bg_attention then returns
+//           BG_E_DEVICE and resets the workspace).
 // Sink mode reads unroped K and rotates it at read by the slot's logical (or absolute) position
 // (attention_sg_roll.wgsl:40-51), in f32 before the f16 conversion.
+#include <map>
+#include <mutex>
+#include <utility>
+
 #include "bg_kernels.h"
 
 namespace bg {
@@ -99,7 +107,10 @@ struct DecodeParams {
   // of o, then (m, l, -, -). Every slot holds kPartialEmpty except between a split's store and
   // the merger's read of it in the same launch.
   float4* ws;
-  int n_mergers;       // splits 0 .. n_mergers-1 also merge units u = split, split + n_mergers, ..
+  int n_mergers;       // the last n_mergers splits also merge: merger i takes units i, i + n_mergers, ..
+  unsigned* err;       // host-visible error word: a merger's bounded wait gave up
+  int spin_limit;      // poll rounds before a merger gives up
+  int withhold_split;  // test hook: this split stores no partial (-1: none)
 };
 
 // "not written yet" marker of a partial slot: a quiet NaN with a payload that arithmetic on
@@ -677,7 +688,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
         for (int e = 0; e < 4; e++) r[e] = r[e] / (1.0f + expf(-gr[e]));
       }
       *(float4*)(p.out + ((size_t)s * p.H + h) * D + d) = make_float4(r[0], r[1], r[2], r[3]);
-    } else {
+    } else if (split != p.withhold_split) {
       const int slot = ((rho * UPR + d / 64) * NS + split) * kUnitF4;
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4v, acc), wrs, (slot + (d % 64) / 4) * 16, 0, kSC1);
       if (d % 64 == 0) {
@@ -686,12 +697,16 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
       }
     }
   }
-  if (single || split >= p.n_mergers) return;
+  const int first_merger = NS - p.n_mergers;
+  if (single || split < first_merger) return;
 
-  // ---------------- merge (splits 0 .. n_mergers-1) ----------------
+  // ---------------- merge (the last n_mergers splits) ----------------
   // A merger polls its unit's slots of every split until none holds kPartialEmpty (the data
   // itself is the completion signal: no flag, ticket or store acknowledgement to wait for), merges
   // them by log-sum-exp, stores the output, and writes kPartialEmpty back for the next launch.
+  // Mergers are the highest split indices, so workgroups are dispatched before the mergers that
+  // wait on them; the host also sizes the grid to fit the GPU at once. The wait is bounded
+  // (p.spin_limit rounds): a merger that gives up stores NaN and raises p.err.
   // Thread (k, c) holds float4 column c of splits k, k + KG, .. (MAXL at a time); wave 0 also
   // holds (m, l) of every split, one per lane.
   constexpr int KG = NTHR / 16;                // split groups
@@ -701,16 +716,17 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
   float* wts = (float*)smem;                                   // [NS]
   float4* red = (float4*)(smem + (((size_t)NS * 4 + 15) & ~(size_t)15));  // [NW][16]
   const u32x4v empty4 = {kPartialEmpty, kPartialEmpty, kPartialEmpty, kPartialEmpty};
-  for (int u = split; u < units; u += p.n_mergers) {
+  bool gave_up = false;  // workgroup-uniform (every exit of poll is a block-wide vote)
+  for (int u = split - first_merger; u < units; u += p.n_mergers) {
     const int rho = u / UPR, d0 = (u % UPR) * 64;
     const int ubase = u * NS * kUnitF4;
     floatx4 v[MAXL];
     float2 ml[MLC];
     // poll batch b0 of the o slots (wave 0 also the (m, l) slots) until nothing is missing;
     // bounded: every split of the grid runs to completion on its own, so the data arrives, and
-    // the bound only guarantees an exit
-    auto poll = [&](int b0, bool with_ml) {
-      for (int it = 0; it < (1 << 20); it++) {
+    // the bound only guarantees an exit. Returns false when the bound ran out.
+    auto poll = [&](int b0, bool with_ml) -> bool {
+      for (int it = 0; it < p.spin_limit; it++) {
         bool missing = false;
 #pragma unroll
         for (int i = 0; i < MAXL; i++) {
@@ -734,9 +750,10 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
         for (int i = 0; i < MAXL; i++)
 #pragma unroll
           for (int e = 0; e < 4; e++) missing = missing || __float_as_uint(v[i][e]) == kPartialEmpty;
-        if (!__syncthreads_or(missing)) break;
+        if (!__syncthreads_or(missing)) return true;
         __builtin_amdgcn_s_sleep(1);
       }
+      return false;
     };
     // consume a batch: weighted sum, then mark its slots empty again
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -754,7 +771,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
         }
       }
     };
-    poll(0, true);
+    gave_up = !poll(0, true) || gave_up;
     if (wave == 0) {
       float M = -INFINITY;
 #pragma unroll
@@ -776,7 +793,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     __syncthreads();
     consume(0);
     for (int b0 = KG * MAXL; b0 < NS; b0 += KG * MAXL) {
-      poll(b0, false);
+      gave_up = !poll(b0, false) || gave_up;
       consume(b0);
     }
     // the four split groups of a wave hold the same column in lanes l, l^16, l^32, l^48: two
@@ -809,10 +826,13 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
 #pragma unroll
         for (int e = 0; e < 4; e++) r[e] = r[e] / (1.0f + expf(-gr[e]));
       }
+      if (gave_up) r[0] = r[1] = r[2] = r[3] = __builtin_nanf("");
       *(float4*)(p.out + ((size_t)s * p.H + h) * D + d) = make_float4(r[0], r[1], r[2], r[3]);
     }
     __syncthreads();
   }
+  // one vector store from one lane, system scope: the host reads the word without a copy
+  if (gave_up && tid == 0) __hip_atomic_store(p.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 static int nset_for(int R) { return (R + 15) / 16; }
@@ -839,22 +859,62 @@ bool decode_supported(const LayerView& L, int S, int H) {
   return R >= 1 && nset_for(R) <= 3 && decode_lds_bytes(L.D, L.dtype, R, nw_max) <= kDecodeLdsMax;
 }
 
-struct Split { int n_tiles, tps, n_splits, n_scan, phys_limit; };
-
-static Split plan_split(const LayerView& L, int S, int pos_base, int num_cus, int nw) {
-  Split s;
+// Split-K plan of one decode launch. Waves: D=128 single-set shapes run 8-wave workgroups (every
+// wave takes at least one tile) when each CU gets 8 tiles or more, otherwise 4-wave workgroups,
+// which split a short range over twice as many CUs. Splits: one workgroup per CU,
+// tiles_per_split = ceil(tiles * KV / CUs), at least one tile per wave, at most kMaxSplits
+// splits. Residency: the merge needs every split to run, so the grid is capped at the
+// workgroups the GPU holds at once (resident_per_cu x CUs, from the kernel's occupancy); below
+// two splits per kv head there is a single split and no merge.
+bool decode_plan(const LayerView& L, int S, int H, int pos_base, int num_cus, int resident_per_cu, DecodePlan* out) {
+  if (!decode_supported(L, S, H)) return false;
+  DecodePlan s;
+  const int R = (H / L.kv_heads) * S;
+  s.nset = nset_for(R);
+  s.passes = (R + 3) / 4;
   s.n_scan = (L.ring.roll && L.ring.head != 0) ? L.max_seq : pos_base + S;
   s.phys_limit = L.ring.roll ? L.max_seq : L.cap;
   s.n_tiles = (s.n_scan + 31) / 32;
   const int cus = num_cus > 0 ? num_cus : 256;
-  // one workgroup per CU: tiles_per_split = ceil(tiles * KV / CUs), at least one tile per wave
+  s.waves = (L.D == 128 && s.nset == 1 && (long)s.n_tiles * L.kv_heads >= 8L * cus) ? 8 : 4;
   int tps = (s.n_tiles * L.kv_heads + cus - 1) / cus;
-  tps = tps < nw ? nw : tps;
+  tps = tps < s.waves ? s.waves : tps;
   const int tps_min = (s.n_tiles + kMaxSplits - 1) / kMaxSplits;
   tps = tps < tps_min ? tps_min : tps;
-  s.tps = tps;
-  s.n_splits = (s.n_tiles + tps - 1) / tps;
-  return s;
+  int ns = (s.n_tiles + tps - 1) / tps;
+  const long resident = (long)(resident_per_cu > 0 ? resident_per_cu : 1) * cus;
+  const int max_splits = (int)(resident / L.kv_heads);
+  if (max_splits < 2) {
+    tps = s.n_tiles;
+    ns = 1;
+  } else if (ns > max_splits) {
+    tps = (s.n_tiles + max_splits - 1) / max_splits;
+    ns = (s.n_tiles + tps - 1) / tps;
+  }
+  s.tiles_per_split = tps;
+  s.n_splits = ns;
+  const int units = R * (L.D / 64);  // merge units: one row x 64 dims
+  s.n_mergers = ns > 1 ? (units < ns ? units : ns) : 0;
+  s.grid = ns * L.kv_heads;
+  *out = s;
+  return true;
+}
+
+// workgroups of one decode instantiation that fit a CU at once with `smem` bytes of dynamic
+// LDS (cached per kernel and size)
+static int resident_blocks(const void* fn, int threads, size_t smem) {
+  static std::mutex mu;
+  static std::map<std::pair<const void*, size_t>, int> memo;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = memo.find({fn, smem});
+  if (it != memo.end()) return it->second;
+  int nb = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fn, threads, smem) != hipSuccess || nb < 1) {
+    (void)hipGetLastError();
+    nb = 1;
+  }
+  memo[{fn, smem}] = nb;
+  return nb;
 }
 
 uint32_t decode_workspace_empty() { return kPartialEmpty; }
@@ -874,14 +934,33 @@ size_t decode_workspace_floats(const LayerView& L, int S, int H, int num_cus, si
 template <int D, int DT, bool ROLL, int NSET, int NPT, int NW>
 static hipError_t launch_cfg(const LayerView& L, const AttnArgs& a, hipStream_t st) {
   using SM = DecodeSmem<D, DT, ROLL, NSET, NW>;
-  const Split sp = plan_split(L, a.S, a.pos_base, a.num_cus, NW);
+  const void* fn = (const void*)decode_kernel<D, DT, ROLL, NSET, NW, NPT>;
+  const int R = (a.H / L.kv_heads) * a.S;
+  const int NP = (R + 3) / 4;
+  size_t smem = SM::total(NP, R);
+  if (smem != decode_lds_bytes(D, DT, R, NW)) return hipErrorInvalidValue;  // the two plans agree
+  // the merge reuses the space: weights [NS] (16-byte aligned) and [waves][16] float4
+  const size_t merge_max = (((size_t)kMaxSplits * 4 + 15) & ~(size_t)15) + (size_t)NW * 16 * 16;
+  smem = smem > merge_max ? smem : merge_max;
+  if (smem > kDecodeLdsMax) return hipErrorInvalidValue;
+  if (smem > 64 * 1024) {
+    static size_t attr_bytes = 0;
+    if (smem > attr_bytes) {
+      hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+      if (e != hipSuccess) return e;
+      attr_bytes = smem;
+    }
+  }
+  DecodePlan sp;
+  if (!decode_plan(L, a.S, a.H, a.pos_base, a.num_cus, resident_blocks(fn, 64 * NW, smem), &sp)) return hipErrorInvalidValue;
+  if (sp.waves != NW || sp.nset != NSET || (NPT > 0 && sp.passes != NPT)) return hipErrorInvalidValue;
   DecodeParams p;
   p.L = L;
   p.q = a.q;
   p.S = a.S;
   p.H = a.H;
   p.G = a.H / L.kv_heads;
-  p.R = p.G * a.S;
+  p.R = R;
   p.pos_base = a.pos_base;
   p.qscale = a.scale * kLog2e * (SM::QUARTER ? (1.0f / 127.0f) : 1.0f);
   p.gate = a.gate;
@@ -890,48 +969,31 @@ static hipError_t launch_cfg(const LayerView& L, const AttnArgs& a, hipStream_t 
   p.n_scan = sp.n_scan;
   p.phys_limit = sp.phys_limit;
   p.n_tiles = sp.n_tiles;
-  p.tiles_per_split = sp.tps;
+  p.tiles_per_split = sp.tiles_per_split;
   p.n_splits = sp.n_splits;
-  const int units = p.R * (D / 64);  // merge units: one row x 64 dims
+  const int units = R * (D / 64);
   const size_t need = (size_t)L.kv_heads * units * sp.n_splits * kUnitF4 * 4;
-  if (sp.n_splits > 1 && (a.ws_o == nullptr || need > a.ws_floats || sp.n_splits > kMaxSplits)) return hipErrorInvalidValue;
+  if (sp.n_splits > 1 && (a.ws_o == nullptr || a.err == nullptr || need > a.ws_floats || sp.n_splits > kMaxSplits))
+    return hipErrorInvalidValue;
   p.ws = (float4*)a.ws_o;
-  p.n_mergers = units < sp.n_splits ? units : sp.n_splits;
-  const int NP = (p.R + 3) / 4;
-  size_t smem = SM::total(NP, p.R);
-  if (smem != decode_lds_bytes(D, DT, p.R, NW)) return hipErrorInvalidValue;  // the two plans agree
-  if (sp.n_splits > 1) {
-    // the merge reuses the space: weights [NS] (16-byte aligned) and [waves][16] float4
-    const size_t merge = (((size_t)sp.n_splits * 4 + 15) & ~(size_t)15) + (size_t)NW * 16 * 16;
-    smem = smem > merge ? smem : merge;
-  }
-  if (smem > kDecodeLdsMax) return hipErrorInvalidValue;
-  if (smem > 64 * 1024) {
-    static size_t attr_bytes = 0;
-    if (smem > attr_bytes) {
-      hipError_t e = hipFuncSetAttribute((const void*)decode_kernel<D, DT, ROLL, NSET, NW, NPT>,
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
-      if (e != hipSuccess) return e;
-      attr_bytes = smem;
-    }
-  }
-  hipLaunchKernelGGL((decode_kernel<D, DT, ROLL, NSET, NW, NPT>), dim3(sp.n_splits * L.kv_heads), dim3(64 * NW), smem, st, p);
+  p.n_mergers = sp.n_mergers;
+  p.err = a.err;
+  p.spin_limit = a.spin_limit > 0 ? a.spin_limit : (1 << 20);
+  p.withhold_split = a.withhold_split;
+  hipLaunchKernelGGL((decode_kernel<D, DT, ROLL, NSET, NW, NPT>), dim3(sp.grid), dim3(64 * NW), smem, st, p);
   return hipGetLastError();
 }
 
 template <int D, int DT, bool ROLL>
 static hipError_t launch_nset(const LayerView& L, const AttnArgs& a, int nset, hipStream_t st) {
-  const int np = ((a.H / L.kv_heads) * a.S + 3) / 4;  // passes of 4 query rows
+  DecodePlan pl;
+  if (!decode_plan(L, a.S, a.H, a.pos_base, a.num_cus, 1, &pl)) return hipErrorInvalidValue;
+  const int np = pl.passes;  // passes of 4 query rows
   switch (nset) {
     case 1: {
-      // decode shapes (G = 4 or 6 rows) get straight-line passes. D=128 runs 8-wave workgroups
-      // (every wave takes at least one tile) when each CU gets 8 tiles or more; a shorter range
-      // runs 4-wave workgroups, which split it over twice as many CUs
-      const int n_scan = (L.ring.roll && L.ring.head != 0) ? L.max_seq : a.pos_base + a.S;
-      const long tiles = (long)(n_scan + 31) / 32 * L.kv_heads;
-      const int cus = a.num_cus > 0 ? a.num_cus : 256;
+      // decode shapes (G = 4 or 6 rows) get straight-line passes
       if constexpr (D == 128) {
-        if (tiles >= 8L * cus) {
+        if (pl.waves == 8) {
           if (np == 1) return launch_cfg<D, DT, ROLL, 1, 1, 8>(L, a, st);
           if (np == 2) return launch_cfg<D, DT, ROLL, 1, 2, 8>(L, a, st);
           return launch_cfg<D, DT, ROLL, 1, 0, 8>(L, a, st);

@@ -12,10 +12,18 @@
  *   - `stream` is a hipStream_t passed as void* (NULL = the default stream). Work is enqueued
  *     in order on that stream; calls return before the GPU finishes unless stated otherwise.
  *   - A cache object is not re-entrant: calls on one cache must be serialized by the caller
- *     (the reference serializes every engine op through one promise chain, src/engine.ts:2877-2887).
- *   - Kernels never allocate. Host-side allocations happen only in bg_kv_create, bg_kv_grow and
- *     bg_attention_reserve (or lazily, once, on the first bg_attention that needs more workspace
- *     or, for a q8 cache, the f16 copy a long prefill runs on).
+ *     (the reference serializes every engine op through one promise chain, src/engine.ts:2877-2887),
+ *     and all GPU work on one cache must be ordered on ONE stream: the layers of a cache share
+ *     one split workspace and one f16 prefill copy, so two bg_attention calls on different
+ *     streams could overlap on the GPU and corrupt each other's partials.
+ *   - Kernels never allocate. Host-side allocations happen only in bg_kv_create, bg_kv_grow,
+ *     bg_attention_reserve, lazily on the first bg_attention that needs more workspace or, for a
+ *     q8 cache, the f16 copy a long prefill runs on, and in the snapshot transfers (a staging
+ *     buffer kept by the cache, grown when a larger region is transferred).
+ *   - The decode kernel's split merge waits a bounded time for the partials of its own grid.
+ *     If a wait gives up (the GPU shared with work that keeps the grid from running at once),
+ *     that launch stores NaN and raises the cache's error word; the next bg_attention on the
+ *     cache, or bg_stream_sync, returns BG_E_DEVICE once and resets the workspace.
  *
  * Storage modes mirror EngineOptions.kvCache (src/types.ts:143-154): f32, f16 (one RNE rounding
  * at write, shaders/copy_kv16.wgsl:13) and q8 (int8 codes + one f32 scale per 32 values,
@@ -72,8 +80,19 @@ int32_t bg_evict_plan(int32_t fill, int32_t need, int32_t sinks, int32_t max_seq
  * (src/engine.ts:1206-1209) as pure index arithmetic. */
 int32_t bg_ring_map(int32_t sinks, int32_t max_seq_len, int32_t head, int32_t logical, int32_t* physical);
 
-/* Synchronize a stream (NULL = device). */
+/* Synchronize a stream (NULL = device). Also reports (BG_E_DEVICE, once) a decode split merge
+ * on any live cache that gave up waiting, after resetting that cache's workspace. */
 int32_t bg_stream_sync(void* stream);
+
+/* Host-only diagnostic with no counterpart in the reference (the WebGPU kernels have no
+ * split-K): the plan bg_attention's split-K decode kernel uses for S query rows of H heads at
+ * positions pos_base.. over a plain cache of kv_heads x head_dim (dtype BG_KV_F16 or
+ * BG_KV_Q8), on num_cus CUs holding resident_per_cu of its workgroups at once. out[0..5] =
+ * waves per workgroup, splits per kv head, 32-slot tiles per split, merging splits per kv
+ * head (the last ones), grid size, tiles. The grid never exceeds resident_per_cu * num_cus.
+ * BG_E_UNSUPPORTED when the shape goes to another kernel. */
+int32_t bg_decode_plan(int32_t kv_heads, int32_t head_dim, int32_t dtype, int32_t S, int32_t H,
+                       int32_t pos_base, int32_t num_cus, int32_t resident_per_cu, int32_t* out);
 
 /* ---- streams and event timing -------------------------------------------------------------
  * For hosts without a GPU runtime of their own (the N-API addon): the reference runs every

@@ -169,3 +169,51 @@ def test_restore_lengths_and_delta_prefix():
         _validate(d, roll=False, cache_len=12, history=list(range(12)))
     with pytest.raises(_lib.BitgpuError, match=r"prefix does not match the current prewarm \(token 3\)"):
         _validate(d, roll=False, cache_len=10, history=[0, 1, 2, 7, 4, 5, 6, 7, 8, 9])
+
+
+# ---------------------------------------------------------------- decode split plan
+def _plan(KV, D, S, H, pos_base, cus=256, resident=1, dtype=_lib.BG_KV_Q8):
+    out = (C.c_int32 * 6)()
+    rc = _lib.lib().bg_decode_plan(KV, D, dtype, S, H, pos_base, cus, resident, out)
+    return rc, list(out)
+
+
+# every decode shape the GPU tests run (kv heads, head_dim, rows S, heads H, attended positions)
+_DECODE_SHAPES = [(8, 128, 1, 32, L) for L in (1, 31, 32, 33, 517, 4096, 4097, 16384, 32768)] + [
+    (16, 128, 1, 16, 777), (8, 128, 1, 64, 777), (4, 256, 1, 24, 777), (8, 256, 1, 8, 777), (2, 128, 1, 16, 777),
+    (4, 256, 1, 24, 4097), (2, 128, 1, 16, 32768), (2, 128, 1, 2, 32768), (1, 256, 1, 4, 32768),
+    (8, 128, 12, 32, 4108), (8, 128, 5, 32, 4000), (8, 128, 5, 32, 3749), (4, 256, 2, 24, 902), (4, 256, 3, 24, 903),
+    (4, 256, 1, 24, 8193), (3, 128, 1, 12, 32768), (5, 128, 1, 20, 20000), (8, 128, 1, 32, 3745)]
+
+
+@pytest.mark.parametrize("KV,D,S,H,L", _DECODE_SHAPES)
+@pytest.mark.parametrize("resident", [1, 2])
+def test_decode_plan_covers_tiles_and_fits_the_gpu(KV, D, S, H, L, resident):
+    """The split-K plan: the splits cover every tile exactly once, the grid never exceeds what
+    the GPU holds at once (the merge waits on splits of its own grid), the merging splits are
+    min(units, splits) and the wave count follows the tiles-per-CU rule."""
+    cus = 256
+    rc, (waves, ns, tps, nm, grid, tiles) = _plan(KV, D, S, H, L - S, cus, resident)
+    assert rc == 0
+    assert tiles == (L + 31) // 32
+    assert ns * tps >= tiles and (ns - 1) * tps < tiles           # every tile, no empty split
+    assert grid == ns * KV <= resident * cus
+    R = (H // KV) * S
+    units = R * (D // 64)
+    assert nm == (min(units, ns) if ns > 1 else 0)
+    assert ns <= 256
+    if ns > 1:
+        assert tps >= waves                                        # every wave has a tile
+    nset = (R + 15) // 16
+    assert waves == (8 if D == 128 and nset == 1 and tiles * KV >= 8 * cus else 4)
+
+
+def test_decode_plan_residency_cap():
+    # 3 kv heads on 256 CUs at one workgroup a CU: ceil-splitting alone would give 86 x 3 = 258
+    rc, (waves, ns, tps, nm, grid, tiles) = _plan(3, 128, 1, 12, 32767, 256, 1)
+    assert rc == 0 and grid <= 256 and tps == 13 and ns == 79    # tiles per split raised 12 -> 13
+    # a GPU that holds fewer workgroups than two splits per kv head runs one split, no merge
+    rc, (waves, ns, tps, nm, grid, tiles) = _plan(8, 128, 1, 32, 32767, 8, 1)
+    assert rc == 0 and ns == 1 and nm == 0 and tps == tiles
+    # shapes the decode kernel does not take
+    assert _plan(8, 128, 64, 32, 1000)[0] == _lib.BG_E_UNSUPPORTED
