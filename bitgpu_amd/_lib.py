@@ -49,6 +49,7 @@ SIGNATURES = [
     ("bg_qkv_prologue", _i32, [_vp, _i32, _vp, _i32, _vp, _vp, _i32, _i32, _vp, _vp, _f32,
                                _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp]),
     ("bg_attention", _i32, [_vp, _i32, _vp, _i32, _i32, _i32, _f32, _vp, _i32, _vp, _vp]),
+    ("bg_attention_noalloc", _i32, [_vp, _i32, _vp, _i32, _i32, _i32, _f32, _vp, _i32, _vp, _vp]),
     ("bg_attention_reserve", _i32, [_vp, _i32, _i32]),
     ("bg_kv_evict", _i32, [_vp, _i32, _i32, _pi32]),
     ("bg_kv_evict_for", _i32, [_vp, _i32, _i32, _pi32]),

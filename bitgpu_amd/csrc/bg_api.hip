@@ -117,6 +117,23 @@ void free_layers(std::vector<void*>& k, std::vector<void*>& v, std::vector<float
 // slots the caller may address: the window in sink mode, the grown capacity otherwise
 int addressable(const bg_kv_cache* c) { return c->roll ? c->max_seq : c->capacity; }
 
+// ---- the allocation-free entry point's scratch ------------------------------------------------
+// bg_attention_noalloc keeps the decode kernel's split partials here instead of in a workspace
+// the library allocates: one array per GPU, held until the process ends. Host code never passes
+// the array's name to a kernel (on the host it is a stand-in, not a device address): the device
+// address comes from hipGetSymbolAddress, once per device, and only that pointer is used.
+// Between launches every slot holds the decode kernel's empty marker; the set-up fills it once.
+constexpr size_t kScratchBytes = (size_t)8 << 20;  // 8 MiB per GPU
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+__global__ void fill_u32_kernel(uint32_t* p, uint32_t value, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    p[i] = value;
+}
+
 // live caches, for bg_stream_sync's check of their merge error words
 std::mutex g_caches_mu;
 std::set<bg_kv_cache*> g_caches;
@@ -146,6 +163,13 @@ int32_t take_merge_error(bg_kv_cache* c, hipStream_t st) {
   hipError_t e = hipDeviceSynchronize();
   if (e == hipSuccess && c->ws)
     e = hipMemsetD32((hipDeviceptr_t)c->ws, (int)bg::decode_workspace_empty(), c->ws_floats);
+  int dev = 0;
+  if (e == hipSuccess) e = hipGetDevice(&dev);
+  if (e == hipSuccess && dev >= 0 && dev < kMaxDevices) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev])
+      e = hipMemsetD32((hipDeviceptr_t)g_scratch_ptr[dev], (int)bg::decode_workspace_empty(), kScratchBytes / 4);
+  }
   if (e == hipSuccess) e = hipDeviceSynchronize();
   if (e != hipSuccess) return hip_fail(e, "workspace reset after a merge timeout");
   __atomic_store_n(c->err_host, 0u, __ATOMIC_RELEASE);
@@ -575,8 +599,9 @@ int32_t bg_attention_reserve(bg_kv_cache* c, int32_t S, int32_t H) {
   return ensure_workspace(c, S, H);
 }
 
-int32_t bg_attention(bg_kv_cache* c, int32_t layer, const float* q, int32_t S, int32_t H, int32_t pos_base, float scale,
-                     const float* gate, int32_t gate_stride, float* out, void* stream) {
+// Argument checks shared by bg_attention and bg_attention_noalloc.
+static int32_t check_attention_args(bg_kv_cache* c, int32_t layer, const float* q, int32_t S, int32_t H,
+                                    int32_t pos_base, float scale, const float* gate, int32_t gate_stride, float* out) {
   if (!c || !q || !out) return fail(BG_E_INVALID, "bg_attention: NULL argument");
   if (layer < 0 || layer >= c->n_layers) return fail(BG_E_INVALID, "bg_attention: layer %d out of range", layer);
   if (S < 1 || H < 1 || H % c->kv_heads) return fail(BG_E_INVALID, "bg_attention: S %d, heads %d (kv_heads %d)", S, H, c->kv_heads);
@@ -592,10 +617,11 @@ int32_t bg_attention(bg_kv_cache* c, int32_t layer, const float* q, int32_t S, i
     if (c->rope_positions < need)
       return fail(BG_E_INVALID, "bg_attention: rope table has %d rows, read-time rotation needs %ld", c->rope_positions, need);
   }
-  hipStream_t st = (hipStream_t)stream;
-  int32_t rc0 = take_merge_error(c, st);
-  if (rc0 != BG_OK) return rc0;
-  LayerView L = view(c, layer);
+  return BG_OK;
+}
+
+static bg::AttnArgs attention_args(bg_kv_cache* c, const float* q, int32_t S, int32_t H, int32_t pos_base, float scale,
+                                   const float* gate, int32_t gate_stride, float* out) {
   bg::AttnArgs a;
   a.q = q;
   a.S = S;
@@ -615,6 +641,18 @@ int32_t bg_attention(bg_kv_cache* c, int32_t layer, const float* q, int32_t S, i
   a.err = c->err_dev;
   a.spin_limit = env_int("BG_DEBUG_MERGE_SPIN", 0);
   a.withhold_split = env_int("BG_DEBUG_WITHHOLD_SPLIT", -1);
+  return a;
+}
+
+int32_t bg_attention(bg_kv_cache* c, int32_t layer, const float* q, int32_t S, int32_t H, int32_t pos_base, float scale,
+                     const float* gate, int32_t gate_stride, float* out, void* stream) {
+  int32_t rc0 = check_attention_args(c, layer, q, S, H, pos_base, scale, gate, gate_stride, out);
+  if (rc0 != BG_OK) return rc0;
+  hipStream_t st = (hipStream_t)stream;
+  rc0 = take_merge_error(c, st);
+  if (rc0 != BG_OK) return rc0;
+  LayerView L = view(c, layer);
+  bg::AttnArgs a = attention_args(c, q, S, H, pos_base, scale, gate, gate_stride, out);
   hipError_t e;
   if (c->dtype == BG_KV_F32 && bg::f32_split_supported(L, S, H)) {
     int32_t rc = ensure_workspace(c, S, H);
@@ -652,6 +690,63 @@ int32_t bg_attention(bg_kv_cache* c, int32_t layer, const float* q, int32_t S, i
     }
   } else {
     return fail(BG_E_UNSUPPORTED, "bg_attention: no kernel for S %d, heads %d", S, H);
+  }
+  return e == hipSuccess ? BG_OK : hip_fail(e, "attention launch");
+}
+
+int32_t bg_attention_noalloc(bg_kv_cache* c, int32_t layer, const float* q, int32_t S, int32_t H, int32_t pos_base,
+                             float scale, const float* gate, int32_t gate_stride, float* out, void* stream) {
+  int32_t rc = check_attention_args(c, layer, q, S, H, pos_base, scale, gate, gate_stride, out);
+  if (rc != BG_OK) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "bg_attention_noalloc: current device");
+  if (dev < 0 || dev >= kMaxDevices) return fail(BG_E_UNSUPPORTED, "bg_attention_noalloc: device %d beyond %d", dev, kMaxDevices);
+  void* ptr = nullptr;
+  {
+    // set-up, once per device with that device current: the array's device address, then
+    // every slot set to the empty marker (a fill kernel, completed before first use)
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+      if (capturing(st))
+        return fail(BG_E_STATE, "bg_attention_noalloc: the first call on a device sets up its scratch and "
+                                "cannot be captured; call it once outside graph capture");
+      void* p = nullptr;
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !p) return hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol, "scratch symbol address");
+      hipLaunchKernelGGL(fill_u32_kernel, dim3(256), dim3(256), 0, st, (uint32_t*)p, bg::decode_workspace_empty(),
+                         kScratchBytes / 4);
+      e = hipGetLastError();
+      if (e == hipSuccess) e = st ? hipStreamSynchronize(st) : hipDeviceSynchronize();
+      if (e != hipSuccess) return hip_fail(e, "scratch set-up");
+      g_scratch_ptr[dev] = p;
+    }
+    ptr = g_scratch_ptr[dev];
+  }
+  rc = take_merge_error(c, st);
+  if (rc != BG_OK) return rc;
+  LayerView L = view(c, layer);
+  bg::AttnArgs a = attention_args(c, q, S, H, pos_base, scale, gate, gate_stride, out);
+  if (c->dtype == BG_KV_F32) {
+    // the exact-f32 kernel of one wave per (query, head) keeps no partials
+    e = bg::launch_attention_f32(L, a, st);
+  } else if (bg::decode_supported(L, S, H)) {
+    bg::DecodePlan pl;
+    // the most splits any occupancy gives (a lower residency only merges splits)
+    if (!bg::decode_plan(L, S, H, pos_base, c->num_cus, 1 << 20, &pl)) return fail(BG_E_UNSUPPORTED, "decode plan");
+    const size_t need = bg::decode_partial_floats(L, S, H, pl.n_splits) * sizeof(float);
+    if (pl.n_splits > 1 && need > kScratchBytes)
+      return fail(BG_E_INVALID, "bg_attention_noalloc: the split partials of S %d, heads %d over %d positions need %zu "
+                                "bytes, beyond the %zu-byte scratch (use bg_attention)", S, H, pos_base + S, need, kScratchBytes);
+    a.ws_o = (float*)ptr;
+    a.ws_floats = kScratchBytes / sizeof(float);
+    e = bg::launch_attention_decode(L, a, st);
+  } else if (bg::prefill_supported(L, S, H)) {
+    // a q8 cache is staged in-kernel (no f16 copy): the same values, so the same results
+    e = bg::launch_attention_prefill(L, a, st);
+  } else {
+    return fail(BG_E_UNSUPPORTED, "bg_attention_noalloc: no kernel for S %d, heads %d", S, H);
   }
   return e == hipSuccess ? BG_OK : hip_fail(e, "attention launch");
 }

@@ -75,6 +75,8 @@ hipError_t launch_attention_prefill(const LayerView& L, const AttnArgs& a, hipSt
 // with the 32-bit pattern decode_workspace_empty() before its first use
 size_t decode_workspace_floats(const LayerView& L, int S, int H, int num_cus, size_t* counters);
 uint32_t decode_workspace_empty();
+// floats of the split partials one decode launch with n_splits splits per kv head writes
+size_t decode_partial_floats(const LayerView& L, int S, int H, int n_splits);
 bool decode_supported(const LayerView& L, int S, int H);
 // the split-K plan of a decode launch (host-only arithmetic; false when the kernel does not take
 // the shape). resident_per_cu: workgroups of the launch's instantiation a CU holds at once.

@@ -919,6 +919,11 @@ static int resident_blocks(const void* fn, int threads, size_t smem) {
 
 uint32_t decode_workspace_empty() { return kPartialEmpty; }
 
+size_t decode_partial_floats(const LayerView& L, int S, int H, int n_splits) {
+  const int R = (H / L.kv_heads) * S;
+  return (size_t)L.kv_heads * R * (L.D / 64) * n_splits * kUnitF4 * 4;
+}
+
 size_t decode_workspace_floats(const LayerView& L, int S, int H, int num_cus, size_t* counters) {
   // upper bound over every pos_base: tiles_per_split >= 4 waves, so at most cap/32/4 splits
   // (and kMaxSplits); one 17-float4 slot per (kv head, unit, split). The caller fills it with

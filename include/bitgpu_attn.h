@@ -172,6 +172,23 @@ int32_t bg_attention(bg_kv_cache* cache, int32_t layer, const float* q, int32_t 
                      int32_t pos_base, float scale, const float* gate, int32_t gate_stride,
                      float* out, void* stream);
 
+/* Allocation-free variant of bg_attention. No counterpart in the reference (WebGPU dispatches
+ * never allocate per call); it is for callers that cannot call hipMalloc: code under HIP graph
+ * capture, tight serving loops, harnesses that forbid allocation. Same arguments and results as
+ * bg_attention, but it allocates nothing: the decode kernel's split partials live in a
+ * file-scope device array of 8 MiB per GPU (held until the process ends) instead of the
+ * cache's workspace; a q8 prefill stages its tiles in-kernel instead of through the f16 copy
+ * (the same values: identical output); an f32 cache runs the exact-f32 kernel of one wave per
+ * (query, head), which keeps no partials (agrees with bg_attention to f32 rounding). A launch
+ * whose partials would exceed the array is rejected with BG_E_INVALID before anything runs.
+ * The first call on a device sets the array up (a fill kernel, synchronized) and must not be
+ * under graph capture (BG_E_STATE). Every call on one GPU shares that GPU's array: calls that
+ * overlap on the GPU (different streams, or different host threads) race and corrupt each
+ * other's outputs -- order them on one stream. */
+int32_t bg_attention_noalloc(bg_kv_cache* cache, int32_t layer, const float* q, int32_t S, int32_t H,
+                             int32_t pos_base, float scale, const float* gate, int32_t gate_stride,
+                             float* out, void* stream);
+
 /* Pre-size the split-K workspace for up to S query rows of H heads (otherwise sized on first
  * use), and for a q8 cache whose prefill of S rows runs on an f16 copy of the attended slots,
  * allocate that copy. Call before capturing bg_attention into a HIP graph. */
