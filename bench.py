@@ -121,6 +121,67 @@ class DecodeSweep:
         self.cache.close()
 
 
+def blas_info():
+    """numpy's BLAS (numpy.show_config) and the thread settings it runs with."""
+    info = {}
+    try:
+        cfgd = np.show_config(mode="dicts")
+        b = cfgd.get("Build Dependencies", {}).get("blas", {})
+        info = {"name": b.get("name"), "version": b.get("version"), "config": b.get("openblas configuration")}
+    except Exception as e:  # noqa: BLE001 - a report, not a requirement
+        info = {"error": str(e)}
+    try:
+        import threadpoolctl
+        info["threadpools"] = [{"api": t.get("user_api"), "lib": t.get("internal_api"), "threads": t.get("num_threads")}
+                               for t in threadpoolctl.threadpool_info()]
+    except Exception:  # noqa: BLE001
+        pass
+    info["env"] = {k: os.environ[k] for k in ("OMP_NUM_THREADS", "OPENBLAS_NUM_THREADS", "MKL_NUM_THREADS")
+                   if k in os.environ}
+    return info
+
+
+def _best(fn, budget_s, reps=5):
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 2:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+        if len(times) >= reps:
+            break
+    return min(times), len(times)
+
+
+def cpu_prefill_samples(W, budget_s=4.0):
+    """The oracle's causal prefill attention for C2 (f16) and C5 (q8, gated) on a bounded sample
+    of query rows (64-row blocks at four depths, tools/reference.py:158-175 and
+    tools/qwen35_numpy.py:102-114 restated); the rate in FLOP/s over the sample's causal pairs
+    gives the full prefill's time."""
+    from oracle import ref
+    out = {}
+    for name, cfg, S in (("c2_prefill_f16", W.C2, W.C2_S), ("c5_prefill_q8", W.C5, W.C5_PREFILL)):
+        q, k, v, g = W.prefill_inputs(cfg, S, 2)
+        kk = ref.kv_roundtrip(k, cfg.kv)
+        vv = ref.kv_roundtrip(v, cfg.kv)
+        blocks = [int(f * S) - 64 if f == 1.0 else int(f * S) for f in (0.25, 0.5, 0.75, 1.0)]
+        scale = 1.0 / np.sqrt(cfg.D) if cfg.gate else None
+
+        def run():
+            for r0 in blocks:
+                rows = slice(r0, r0 + 64)
+                if cfg.gate:
+                    ref.gated_attention(q[rows], kk[:r0 + 64], vv[:r0 + 64], g[rows], r0)
+                else:
+                    ref.attention(q[rows], kk[:r0 + 64], vv[:r0 + 64], r0, scale=scale)
+        best, n = _best(run, budget_s, reps=3)
+        fl = sum(causal_flops(64, cfg.H, cfg.D, past=r0) for r0 in blocks)
+        rate = fl / best
+        out[name] = {"tflops": round(rate / 1e12, 4), "us_full_estimate": round(causal_flops(S, cfg.H, cfg.D) / rate * 1e6, 1),
+                     "sample": f"4 blocks of 64 query rows at depths {blocks} of the S={S} prefill, best of {n}"}
+    return out
+
+
 def cpu_baseline(sweep, W, budget_s=12.0):
     """The oracle numpy path (tools/reference.py:158-175 restated, q8 dequant first) on this
     host's cores, one layer of the headline workload per repetition; best of the repetitions
@@ -146,15 +207,27 @@ def cpu_baseline(sweep, W, budget_s=12.0):
             break
     best = min(times)
     cores = os.cpu_count()
+    blas = blas_info()
+    threads = max([t.get("threads") or 0 for t in blas.get("threadpools", [])] or [cores])
     return {
         "value": round(c3_bytes(L) / best / 1e9, 3),
         "unit": "GB/s",
         "us_per_layer": round(best * 1e6, 1),
-        "cores": cores,
+        "cores": threads,
         "kind": "port",
         "sample": f"one layer of the C3 32k q8 decode (numpy oracle: q8 dequant + GQA softmax attention in "
-                  f"float64), best of {len(times)}; numpy BLAS threads = all {cores} host cores",
+                  f"float64), best of {len(times)}; {threads} BLAS threads on {cores} host cores",
+        "blas": blas,
+        "prefill": cpu_prefill_samples(W),
     }
+
+
+def prologue_bytes(cfg, S):
+    """HBM bytes of the fused prologue for S positions: Q read (the query half of each row) and
+    written as f32, K and V read as f32 and written in the storage format (+ q8 scales)."""
+    eb = {"f32": 4, "f16": 2, "q8": 1}[cfg.kv]
+    sc = 2 * S * cfg.KV * (cfg.D // 32) * 4 if cfg.kv == "q8" else 0
+    return 2 * S * cfg.H * cfg.D * 4 + 2 * S * cfg.KV * cfg.D * 4 + 2 * S * cfg.KV * cfg.D * eb + sc
 
 
 def bench_prefill(torch, E, W, cfg, S, steps, warmup, seed):
@@ -183,8 +256,43 @@ def bench_prefill(torch, E, W, cfg, S, steps, warmup, seed):
     us_pro = graph_replay_us(torch, prologue, steps, warmup, per_graph)
     fl = causal_flops(S, cfg.H, cfg.D)
     c.close()
+    pb = prologue_bytes(cfg, S)
     return {"S": S, "attn_us": round(us_attn, 1), "prologue_us": round(us_pro, 1),
-            "tflops": round(fl / us_attn / 1e6, 1), "mfma_frac": round(fl / us_attn / 1e6 / MFMA_F16_PEAK_TFLOPS, 4)}
+            "tflops": round(fl / us_attn / 1e6, 1), "mfma_frac": round(fl / us_attn / 1e6 / MFMA_F16_PEAK_TFLOPS, 4),
+            "prologue_bytes": pb, "prologue_GBs": round(pb / us_pro / 1e3, 1),
+            "prologue_hbm_frac": round(pb / us_pro / 1e3 / HBM_PEAK_GBS, 4)}
+
+
+def make_prologue(torch, E, W, cfg, S, seed=2):
+    """The fused prologue of an S-token prefill (Q, K, V) into a fresh cache; (launch, close)."""
+    q, k, v, _ = W.prefill_inputs(cfg, S, seed)
+    dev = "cuda"
+    c = E.KvCache(1, cfg.KV, cfg.D, cfg.kv, max_seq_len=S, capacity=S)
+    cos, sin = (torch.from_numpy(x).to(dev) for x in E.rope_tables(cfg.theta, cfg.rot, S))
+    ones = torch.ones(cfg.D, device=dev)
+    qt, kt, vt = (torch.from_numpy(x).to(dev) for x in (q, k, v))
+    qr = torch.empty(S, cfg.H, cfg.D, device=dev)
+    return (lambda: E.qkv_prologue(c, 0, qt, kt, vt, S, cfg.H, ones, ones, cfg.eps, cos, sin, cfg.rot, 0, 0,
+                                   q_out=qr)), c.close
+
+
+def profile_set(torch, E, W, names, n):
+    """Launch the named kernels n times each with nothing else on the GPU (rocprofv3 --pmc passes)."""
+    for name in names:
+        if name == "decode_c5":
+            fn, _, _, close = make_c5_decode(torch, E, W)
+        elif name in ("decode_c4", "verify_c4"):
+            fn, _, _, close = make_c4(torch, E, W, 1 if name == "decode_c4" else W.C4_VERIFY)
+        elif name == "prologue_c2":
+            fn, close = make_prologue(torch, E, W, W.C2, W.C2_S)
+        elif name == "prologue_c5":
+            fn, close = make_prologue(torch, E, W, W.C5, W.C5_PREFILL)
+        else:
+            raise SystemExit(f"bench.py: unknown --profile-set entry {name}")
+        for _ in range(n):
+            fn()
+        torch.cuda.synchronize()
+        close()
 
 
 def profile_prefill(torch, E, W, n):
@@ -229,61 +337,78 @@ def bench_c1(torch, E, W, steps, warmup):
     return {"us_per_layer": round(us, 2), "GBs": round(B / us / 1e3, 1), "layers": 28}
 
 
-def bench_c4(torch, E, W, steps, warmup):
+def make_c4(torch, E, W, verify):
     """Sink mode at position 100000: the ring state after the reference's greedy eviction
-    schedule (index arithmetic only), f16 cache, 4 sinks + 4096 window."""
+    schedule (index arithmetic only), f16 cache, 4 sinks + 4096 window; `verify` query rows.
+    Returns (launch, algorithmic bytes, resident slots, close)."""
     cfg = W.C4
     sinks, max_seq = cfg.sinks, cfg.sinks + cfg.window
     dev = "cuda"
+    c = E.KvCache(1, cfg.KV, cfg.D, cfg.kv, max_seq_len=max_seq, overflow="sinks", sink_tokens=sinks)
+    fill, fed = 1000, 1000
+    while fed < W.C4_POSITION:
+        batch = min(4, W.C4_POSITION - fed)
+        fill = c.evict_for(fill, batch) + batch
+        fed += batch
+    fill = c.evict_for(fill, verify)
+    cos, sin = (torch.from_numpy(x).to(dev) for x in E.rope_tables(cfg.theta, cfg.rot, max_seq))
+    c.set_rope(cos, sin)
+    rng = np.random.default_rng(4)
+    k = torch.from_numpy(rng.standard_normal((fill + verify, cfg.KV, cfg.D)).astype(np.float32)).to(dev)
+    v = torch.from_numpy(rng.standard_normal((fill + verify, cfg.KV, cfg.D)).astype(np.float32)).to(dev)
+    q = torch.from_numpy(rng.standard_normal((verify, cfg.H, cfg.D)).astype(np.float32)).to(dev)
+    ones = torch.ones(cfg.D, device=dev)
+    E.qkv_prologue(c, 0, None, k, v, fill + verify, cfg.H, None, ones, cfg.eps, cos, sin, cfg.rot, 0, 0)
+    qr = E.qkv_prologue(c, 0, q, None, None, verify, cfg.H, ones, None, cfg.eps, cos, sin, cfg.rot, fill, fill)
+    out = torch.empty(verify, cfg.H, cfg.D, device=dev)
+    B = (fill + verify) * cfg.KV * 2 * cfg.D * 2 + 2 * verify * cfg.H * cfg.D * 4
+    return (lambda: E.attention(c, 0, qr, verify, cfg.H, fill, out=out)), B, fill + verify, c.close
+
+
+def bench_c4(torch, E, W, steps, warmup):
     res = {}
     for verify in (1, W.C4_VERIFY):
-        c = E.KvCache(1, cfg.KV, cfg.D, cfg.kv, max_seq_len=max_seq, overflow="sinks", sink_tokens=sinks)
-        fill, fed = 1000, 1000
-        while fed < W.C4_POSITION:
-            batch = min(4, W.C4_POSITION - fed)
-            fill = c.evict_for(fill, batch) + batch
-            fed += batch
-        fill = c.evict_for(fill, verify)
-        cos, sin = (torch.from_numpy(x).to(dev) for x in E.rope_tables(cfg.theta, cfg.rot, max_seq))
-        c.set_rope(cos, sin)
-        rng = np.random.default_rng(4)
-        k = torch.from_numpy(rng.standard_normal((fill + verify, cfg.KV, cfg.D)).astype(np.float32)).to(dev)
-        v = torch.from_numpy(rng.standard_normal((fill + verify, cfg.KV, cfg.D)).astype(np.float32)).to(dev)
-        q = torch.from_numpy(rng.standard_normal((verify, cfg.H, cfg.D)).astype(np.float32)).to(dev)
-        ones = torch.ones(cfg.D, device=dev)
-        E.qkv_prologue(c, 0, None, k, v, fill + verify, cfg.H, None, ones, cfg.eps, cos, sin, cfg.rot, 0, 0)
-        qr = E.qkv_prologue(c, 0, q, None, None, verify, cfg.H, ones, None, cfg.eps, cos, sin, cfg.rot, fill, fill)
-        out = torch.empty(verify, cfg.H, cfg.D, device=dev)
-        us = graph_replay_us(torch, lambda: E.attention(c, 0, qr, verify, cfg.H, fill, out=out), steps, warmup,
-                             per_graph=16)
-        B = (fill + verify) * cfg.KV * 2 * cfg.D * 2 + 2 * verify * cfg.H * cfg.D * 4
+        fn, B, slots, close = make_c4(torch, E, W, verify)
+        us = graph_replay_us(torch, fn, steps, warmup, per_graph=16)
         res["decode" if verify == 1 else f"verify{verify}"] = {"us": round(us, 2), "GBs": round(B / us / 1e3, 1),
-                                                               "resident_slots": fill + verify}
-        c.close()
+                                                               "hbm_frac": round(B / us / 1e3 / HBM_PEAK_GBS, 4),
+                                                               "resident_slots": slots}
+        close()
     return res
 
 
-def bench_c5_decode(torch, E, W, steps, warmup):
+def make_c5_decode(torch, E, W, layers=16):
+    """C5 decode step at 8193 cached positions over `layers` distinct q8 layers (D=256, gated).
+    Returns (launch of every layer, algorithmic bytes per layer, context, close)."""
     cfg = W.C5
     L = W.C5_PREFILL + 1
     dev = "cuda"
-    c = E.KvCache(16, cfg.KV, cfg.D, cfg.kv, max_seq_len=W.C5_PREFILL + W.C5_DECODE_STEPS,
+    c = E.KvCache(layers, cfg.KV, cfg.D, cfg.kv, max_seq_len=W.C5_PREFILL + W.C5_DECODE_STEPS,
                   capacity=W.C5_PREFILL + W.C5_DECODE_STEPS)
     rng = np.random.default_rng(5)
     k = torch.from_numpy(rng.standard_normal((L, cfg.KV, cfg.D)).astype(np.float32)).to(dev)
     from bitgpu_amd._lib import BG_K, BG_V
-    for li in range(16):
+    for li in range(layers):
         c.append_kv(k, BG_K, li, L * cfg.KV, 0)
         c.append_kv(k, BG_V, li, L * cfg.KV, 0)
     q = torch.from_numpy(rng.standard_normal((1, cfg.H, cfg.D)).astype(np.float32)).to(dev)
     g = torch.from_numpy(rng.standard_normal((1, cfg.H, cfg.D)).astype(np.float32)).to(dev)
     out = torch.empty(1, cfg.H, cfg.D, device=dev)
     scale = float(1.0 / np.sqrt(cfg.D))
-    us = graph_replay_us(torch, lambda: [E.attention(c, li, q, 1, cfg.H, L - 1, scale=scale, gate=g, gate_stride=cfg.D,
-                                                     out=out) for li in range(16)], steps, warmup) / 16
-    c.close()
     B = L * cfg.KV * 2 * (cfg.D + 4 * cfg.D // 32) + 3 * cfg.H * cfg.D * 4
-    return {"context": L, "us_per_layer": round(us, 2), "GBs": round(B / us / 1e3, 1)}
+
+    def run():
+        for li in range(layers):
+            E.attention(c, li, q, 1, cfg.H, L - 1, scale=scale, gate=g, gate_stride=cfg.D, out=out)
+    return run, B, L, c.close
+
+
+def bench_c5_decode(torch, E, W, steps, warmup):
+    run, B, L, close = make_c5_decode(torch, E, W)
+    us = graph_replay_us(torch, run, steps, warmup) / 16
+    close()
+    return {"context": L, "us_per_layer": round(us, 2), "GBs": round(B / us / 1e3, 1),
+            "hbm_frac": round(B / us / 1e3 / HBM_PEAK_GBS, 4)}
 
 
 def load_traffic(name):
@@ -307,6 +432,10 @@ def main():
                     help="run only the headline sweep this many times (for rocprofv3 --pmc), print nothing else")
     ap.add_argument("--profile-prefill", type=int, default=0,
                     help="run only the C2 and C5 prefill attention this many times each (for rocprofv3 --pmc)")
+    ap.add_argument("--profile-set", default="", metavar="NAMES",
+                    help="comma list of decode_c5, decode_c4, verify_c4, prologue_c2, prologue_c5: run only these "
+                         "kernels --profile-n times each (for rocprofv3 --pmc), print nothing else")
+    ap.add_argument("--profile-n", type=int, default=20)
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="run only a device-to-device copy of MIB MiB (3 times) to calibrate the "
@@ -337,6 +466,10 @@ def main():
 
     if args.profile_prefill:
         profile_prefill(torch, E, W, args.profile_prefill)
+        return
+
+    if args.profile_set:
+        profile_set(torch, E, W, [x for x in args.profile_set.split(",") if x], args.profile_n)
         return
 
     L = 32768

@@ -515,6 +515,11 @@ int32_t bg_qkv_prologue(bg_kv_cache* c, int32_t layer, const float* q, int32_t q
     if (pos0 < 0 || (long)pos0 + S > rope_positions)
       return fail(BG_E_INVALID, "bg_qkv_prologue: positions %d..%d outside the %d-row rope table", pos0, pos0 + S - 1, rope_positions);
   }
+  // rows are read and written 16 bytes a lane
+  const uintptr_t mis = ((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)q_out | (uintptr_t)q_gamma |
+                         (uintptr_t)k_gamma | (uintptr_t)cos_tab | (uintptr_t)sin_tab) & 15;
+  if (mis || (q && (q_stride & 3)))
+    return fail(BG_E_INVALID, "bg_qkv_prologue: buffers must be 16-byte aligned and q_stride a multiple of 4");
   if ((k || v) && (slot0 < 0 || slot0 + S > addressable(c)))
     return fail(BG_E_INVALID, "bg_qkv_prologue: slots %d..%d beyond capacity %d", slot0, slot0 + S - 1, addressable(c));
   bg::PrologueArgs a;

@@ -40,8 +40,8 @@ static hipError_t kv_write_d(const LayerView& L, int which, const float* src, in
 
 hipError_t launch_kv_write(const LayerView& L, int which, const float* src, int rows, int dst_row0, hipStream_t st) {
   if (rows <= 0) return hipSuccess;
+  // head_dim is 128 or 256 (bg_kv_create rejects the rest)
   switch (L.D) {
-    case 64: return kv_write_d<64>(L, which, src, rows, dst_row0, st);
     case 128: return kv_write_d<128>(L, which, src, rows, dst_row0, st);
     default: return kv_write_d<256>(L, which, src, rows, dst_row0, st);
   }
@@ -151,7 +151,6 @@ hipError_t launch_kv_dequant_f16(const LayerView& L, int n_slots, void* kdst, vo
   const size_t chunks = 2 * (size_t)n_slots * L.D / 16 * L.kv_heads;
   const int grid = (int)((chunks + 255) / 256 < 4096 ? (chunks + 255) / 256 : 4096);
   switch (L.D) {
-    case 64: hipLaunchKernelGGL((kv_dequant_kernel<64>), dim3(grid), dim3(256), 0, st, L, n_slots, (__half*)kdst, (__half*)vdst); break;
     case 128: hipLaunchKernelGGL((kv_dequant_kernel<128>), dim3(grid), dim3(256), 0, st, L, n_slots, (__half*)kdst, (__half*)vdst); break;
     default: hipLaunchKernelGGL((kv_dequant_kernel<256>), dim3(grid), dim3(256), 0, st, L, n_slots, (__half*)kdst, (__half*)vdst); break;
   }

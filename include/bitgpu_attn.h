@@ -151,7 +151,8 @@ int32_t bg_kv_write(bg_kv_cache* cache, int32_t layer, int32_t which, const floa
  * V rows are stored unchanged at slot0 + s. Tables cos_tab/sin_tab: [rope_positions,
  * rot_dim/2] (the engine's cos/sin caches, indexed by position instead of the per-call [S, D]
  * expansion of ropeBufs, src/engine.ts:994-1009); rot_dim <= head_dim (dims >= rot_dim pass
- * through). */
+ * through). Every buffer is 16-byte aligned and q_stride a multiple of 4 (rows move 16 bytes a
+ * lane); otherwise BG_E_INVALID. */
 int32_t bg_qkv_prologue(bg_kv_cache* cache, int32_t layer, const float* q, int32_t q_stride,
                         const float* k, const float* v, int32_t S, int32_t H,
                         const float* q_gamma, const float* k_gamma, float eps,

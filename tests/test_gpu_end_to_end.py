@@ -7,8 +7,8 @@ things against the oracle run on the same raw draws:
 * the prologue's normed/roped queries, every row (f32, rtol/atol 4e-6: the kernel reduces the
   sum of squares in another order than numpy);
 * the stored keys and values, every row: f32 to 4e-6; f16 within one f16 rounding of the oracle's
-  f32 value (at most 1e-3 of the values may land on the other side of a rounding boundary, one
-  f16 ulp away); q8 codes within one step of ``ref.q8_pack`` of the oracle's keys (again at most
+  f32 value plus 4e-6 (at most 1e-3 of the values may land on the other side of a rounding
+  boundary); q8 codes within one step of ``ref.q8_pack`` of the oracle's keys (again at most
   1e-3 of them) and scales to 4e-6; V (never transformed) bit-exact;
 * the attention output against ``ref.attention`` / ``ref.gated_attention`` over the oracle's own
   stored values (``kv_roundtrip``): max-abs 1e-4 for f32, relative 2e-3 and cosine > 0.99999 for
@@ -58,11 +58,10 @@ def _check_stored(cache, li, base, kn, v_raw):
         want = ref.f16_pack(kn)
         diff = kq.view(np.uint16) != want.view(np.uint16)
         assert diff.mean() <= MISMATCH_FRAC, diff.mean()
-        # a mismatch is the other side of a rounding boundary: one f16 ulp, value within one
-        # f16 rounding of the oracle's f32 key
-        ulp = np.abs(kq.view(np.int16).astype(np.int32) - want.view(np.int16).astype(np.int32))
-        assert ulp.max() <= 1
-        assert np.all(np.abs(kq.astype(np.float32) - kn) <= np.abs(kn) * 2.0 ** -11 + 1e-5)
+        # a mismatch is the other side of a rounding boundary: the stored value is within one
+        # f16 rounding (half an ulp, 2^-11 relative) of the oracle's f32 key plus the f32 noise
+        # of the norm/rope (absolute, where the rotation cancels to a tiny value)
+        assert np.all(np.abs(kq.astype(np.float32) - kn) <= np.abs(kn) * 2.0 ** -11 + F32_ATOL)
         assert np.array_equal(vq.view(np.uint16), ref.f16_pack(v_raw).view(np.uint16))
     else:
         ck, sk = ref.q8_pack(kn)
