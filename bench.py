@@ -411,6 +411,45 @@ def bench_c5_decode(torch, E, W, steps, warmup):
             "hbm_frac": round(B / us / 1e3 / HBM_PEAK_GBS, 4)}
 
 
+def onebit_bytes(N, K):
+    """HBM bytes of one 1-bit GEMV: sign bits, one f32 scale per 128 weights, x and the outputs."""
+    return N * K // 8 + N * (K // 128) * 4 + K * 4 + N * 4
+
+
+def bench_projections(torch, E, steps, warmup, layers=36, HD=4096, H=32, KV=8, D=128):
+    """The decode projections on either side of attention in the Qwen3-8B shape (hidden 4096,
+    32 heads on 8 kv heads, head_dim 128), 36 distinct layers' weights (no cache reuse across
+    launches): the fused qkv projection + prologue into a q8 cache, and o_proj + residual."""
+    rng = np.random.default_rng(7)
+    dev = "cuda"
+    Nq = (H + 2 * KV) * D
+
+    def weight(N, K, N0, N1=0, N2=0):
+        sign = torch.from_numpy(rng.integers(0, 2 ** 32, (N, K // 32), dtype=np.uint64).astype(np.uint32).view(np.int32)).to(dev)
+        sc = torch.from_numpy((np.abs(rng.standard_normal((N, K // 128))) * 0.02).astype(np.float32)).to(dev)
+        return E.OneBitWeight(sign, sc, K, N0, N1, N2)
+    wq = [weight(Nq, HD, H * D, KV * D, KV * D) for _ in range(layers)]
+    wo = [weight(HD, H * D, HD) for _ in range(layers)]
+    c = E.KvCache(layers, KV, D, "q8", max_seq_len=4096, capacity=4096)
+    cos, sin = (torch.from_numpy(x).to(dev) for x in E.rope_tables(1e6, D, 4096))
+    ones = torch.ones(D, device=dev)
+    x = torch.randn(HD, device=dev)
+    h = torch.randn(HD, device=dev)
+    att = torch.randn(H * D, device=dev)
+    q = torch.empty(1, H, D, device=dev)
+    y = torch.empty(HD, device=dev)
+    us_q = graph_replay_us(torch, lambda: [E.qkv_proj_prologue(c, li, x, wq[li], H, ones, ones, 1e-6, cos, sin, D, 1000,
+                                                              1000, q_out=q) for li in range(layers)], steps, warmup) / layers
+    us_o = graph_replay_us(torch, lambda: [E.resid_mm(wo[li], att, h, y) for li in range(layers)], steps, warmup) / layers
+    c.close()
+    bq, bo = onebit_bytes(Nq, HD), onebit_bytes(HD, H * D)
+    return {"qkv_proj_prologue": {"us": round(us_q, 2), "GBs": round(bq / us_q / 1e3, 1),
+                                  "hbm_frac": round(bq / us_q / 1e3 / HBM_PEAK_GBS, 4), "bytes": bq},
+            "o_proj_resid": {"us": round(us_o, 2), "GBs": round(bo / us_o / 1e3, 1),
+                             "hbm_frac": round(bo / us_o / 1e3 / HBM_PEAK_GBS, 4), "bytes": bo},
+            "shape": f"hidden {HD}, {H} heads / {KV} kv heads x {D}, {layers} distinct layers"}
+
+
 def load_traffic(name):
     p = os.path.join(ROOT, "profiles", name)
     if not os.path.exists(p):
@@ -504,6 +543,7 @@ def main():
         extra["c5_decode_q8"] = bench_c5_decode(torch, E, W, args.steps, args.warmup)
         extra["c1_decode_f32"] = bench_c1(torch, E, W, args.steps, args.warmup)
         extra["c4_sinks_f16"] = bench_c4(torch, E, W, args.steps, args.warmup)
+        extra["projections_1bit"] = bench_projections(torch, E, args.steps, args.warmup)
         cpu = cpu_baseline(sweep, W, args.cpu_budget)
     sweep.close()
 

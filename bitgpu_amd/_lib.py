@@ -48,6 +48,10 @@ SIGNATURES = [
     ("bg_kv_write", _i32, [_vp, _i32, _i32, _vp, _i32, _i32, _vp]),
     ("bg_qkv_prologue", _i32, [_vp, _i32, _vp, _i32, _vp, _vp, _i32, _i32, _vp, _vp, _f32,
                                _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp]),
+    ("bg_gemv_split", _i32, [_vp, _i32, _vp, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp]),
+    ("bg_gemv_resid", _i32, [_vp, _i32, _vp, _vp, _i32, _vp, _vp, _vp]),
+    ("bg_qkv_proj_prologue", _i32, [_vp, _i32, _vp, _i32, _vp, _vp, _i32, _vp, _vp, _f32, _vp, _vp, _i32, _i32,
+                                     _i32, _i32, _vp, _vp]),
     ("bg_attention", _i32, [_vp, _i32, _vp, _i32, _i32, _i32, _f32, _vp, _i32, _vp, _vp]),
     ("bg_attention_noalloc", _i32, [_vp, _i32, _vp, _i32, _i32, _i32, _f32, _vp, _i32, _vp, _vp]),
     ("bg_attention_reserve", _i32, [_vp, _i32, _i32]),

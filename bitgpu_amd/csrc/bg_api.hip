@@ -46,6 +46,9 @@ struct bg_kv_cache {
   // snapshot staging buffer (grown on demand, kept until destroy)
   void* stage = nullptr;
   size_t stage_bytes = 0;
+  // fused decode projection: raw K and V rows [2 KV D] and the per-head arrival counters
+  float* proj_raw = nullptr;
+  unsigned* proj_count = nullptr;
 };
 
 namespace {
@@ -113,6 +116,9 @@ void free_layers(std::vector<void*>& k, std::vector<void*>& v, std::vector<float
   for (auto p : vs) if (p) (void)hipFree(p);
   k.clear(); v.clear(); ks.clear(); vs.clear();
 }
+
+// heads (query + key + value) the fused decode projection's arrival counters cover
+constexpr int kProjMaxHeads = 1024;
 
 // slots the caller may address: the window in sink mode, the grown capacity otherwise
 int addressable(const bg_kv_cache* c) { return c->roll ? c->max_seq : c->capacity; }
@@ -370,11 +376,16 @@ int32_t bg_kv_create(int32_t n_layers, int32_t kv_heads, int32_t head_dim, int32
   }
   hipError_t e = hipHostMalloc((void**)&c->err_host, 64, hipHostMallocMapped | hipHostMallocCoherent);
   if (e == hipSuccess) e = hipHostGetDevicePointer((void**)&c->err_dev, c->err_host, 0);
+  if (e == hipSuccess) e = hipMalloc((void**)&c->proj_raw, (size_t)2 * kv_heads * head_dim * sizeof(float));
+  if (e == hipSuccess) e = hipMalloc((void**)&c->proj_count, kProjMaxHeads * sizeof(unsigned));
+  if (e == hipSuccess) e = hipMemset(c->proj_count, 0, kProjMaxHeads * sizeof(unsigned));
   if (e != hipSuccess) {
     if (c->err_host) (void)hipHostFree(c->err_host);
+    if (c->proj_raw) (void)hipFree(c->proj_raw);
+    if (c->proj_count) (void)hipFree(c->proj_count);
     free_layers(c->k, c->v, c->ks, c->vs);
     delete c;
-    return hip_fail(e, "KV cache error word allocation");
+    return hip_fail(e, "KV cache side buffers allocation");
   }
   *c->err_host = 0;
   {
@@ -394,6 +405,8 @@ int32_t bg_kv_destroy(bg_kv_cache* c) {
   (void)hipDeviceSynchronize();
   if (c->err_host) (void)hipHostFree(c->err_host);
   if (c->stage) (void)hipFree(c->stage);
+  if (c->proj_raw) (void)hipFree(c->proj_raw);
+  if (c->proj_count) (void)hipFree(c->proj_count);
   free_layers(c->k, c->v, c->ks, c->vs);
   if (c->ws) (void)hipFree(c->ws);
   if (c->ws_count) (void)hipFree(c->ws_count);
@@ -754,6 +767,76 @@ int32_t bg_attention_noalloc(bg_kv_cache* c, int32_t layer, const float* q, int3
     return fail(BG_E_UNSUPPORTED, "bg_attention_noalloc: no kernel for S %d, heads %d", S, H);
   }
   return e == hipSuccess ? BG_OK : hip_fail(e, "attention launch");
+}
+
+static int32_t check_gemv(const char* who, const float* x, int32_t K, const uint32_t* sign, const float* scales) {
+  if (!x || !sign || !scales) return fail(BG_E_INVALID, "%s: NULL argument", who);
+  if (K < 128 || K % 128) return fail(BG_E_INVALID, "%s: K %d must be a positive multiple of 128", who, K);
+  if (((uintptr_t)x | (uintptr_t)sign | (uintptr_t)scales) & 15)
+    return fail(BG_E_INVALID, "%s: x, sign and scales must be 16-byte aligned", who);
+  return BG_OK;
+}
+
+int32_t bg_gemv_split(const float* x, int32_t K, const uint32_t* sign, const float* scales, int32_t N0, int32_t N1,
+                      int32_t N2, float* out0, float* out1, float* out2, void* stream) {
+  int32_t rc = check_gemv("bg_gemv_split", x, K, sign, scales);
+  if (rc != BG_OK) return rc;
+  if (N0 < 0 || N1 < 0 || N2 < 0 || (N0 && !out0) || (N1 && !out1) || (N2 && !out2))
+    return fail(BG_E_INVALID, "bg_gemv_split: output ranges %d/%d/%d need their buffers", N0, N1, N2);
+  bg::GemvArgs a{x, K, sign, scales, N0, N1, N2, out0, out1, out2, nullptr};
+  hipError_t e = bg::launch_gemv(a, (hipStream_t)stream);
+  return e == hipSuccess ? BG_OK : hip_fail(e, "gemv launch");
+}
+
+int32_t bg_gemv_resid(const float* x, int32_t K, const uint32_t* sign, const float* scales, int32_t N,
+                      const float* resid, float* y, void* stream) {
+  int32_t rc = check_gemv("bg_gemv_resid", x, K, sign, scales);
+  if (rc != BG_OK) return rc;
+  if (N < 0 || !resid || !y) return fail(BG_E_INVALID, "bg_gemv_resid: N %d needs resid and y", N);
+  bg::GemvArgs a{x, K, sign, scales, N, 0, 0, y, nullptr, nullptr, resid};
+  hipError_t e = bg::launch_gemv(a, (hipStream_t)stream);
+  return e == hipSuccess ? BG_OK : hip_fail(e, "gemv launch");
+}
+
+int32_t bg_qkv_proj_prologue(bg_kv_cache* c, int32_t layer, const float* x, int32_t K, const uint32_t* sign,
+                             const float* scales, int32_t H, const float* q_gamma, const float* k_gamma, float eps,
+                             const float* cos_tab, const float* sin_tab, int32_t rope_positions, int32_t rot_dim,
+                             int32_t pos, int32_t slot, float* q_out, void* stream) {
+  if (!c) return fail(BG_E_INVALID, "bg_qkv_proj_prologue: NULL cache");
+  int32_t rc = check_gemv("bg_qkv_proj_prologue", x, K, sign, scales);
+  if (rc != BG_OK) return rc;
+  if (layer < 0 || layer >= c->n_layers) return fail(BG_E_INVALID, "bg_qkv_proj_prologue: layer %d out of range", layer);
+  if (H < c->kv_heads || H % c->kv_heads || H + 2 * c->kv_heads > kProjMaxHeads)
+    return fail(BG_E_INVALID, "bg_qkv_proj_prologue: heads %d (kv_heads %d, at most %d heads in all)", H, c->kv_heads,
+                kProjMaxHeads);
+  if (!q_out || !q_gamma || !k_gamma || !cos_tab || !sin_tab)
+    return fail(BG_E_INVALID, "bg_qkv_proj_prologue: NULL q_out, gamma or rope table");
+  if (((uintptr_t)q_out | (uintptr_t)q_gamma | (uintptr_t)k_gamma | (uintptr_t)cos_tab | (uintptr_t)sin_tab) & 15)
+    return fail(BG_E_INVALID, "bg_qkv_proj_prologue: buffers must be 16-byte aligned");
+  if (rot_dim < 2 || (rot_dim & 1) || rot_dim > c->D) return fail(BG_E_INVALID, "bg_qkv_proj_prologue: bad rot_dim %d", rot_dim);
+  if (pos < 0 || pos >= rope_positions)
+    return fail(BG_E_INVALID, "bg_qkv_proj_prologue: position %d outside the %d-row rope table", pos, rope_positions);
+  if (slot < 0 || slot >= addressable(c))
+    return fail(BG_E_INVALID, "bg_qkv_proj_prologue: slot %d beyond capacity %d", slot, addressable(c));
+  bg::QkvProjArgs a;
+  a.x = x;
+  a.K = K;
+  a.sign = sign;
+  a.scales = scales;
+  a.H = H;
+  a.q_gamma = q_gamma;
+  a.k_gamma = k_gamma;
+  a.eps = eps;
+  a.cos_tab = cos_tab;
+  a.sin_tab = sin_tab;
+  a.rot_dim = rot_dim;
+  a.pos = pos;
+  a.slot = slot;
+  a.q_out = q_out;
+  a.kv_raw = c->proj_raw;
+  a.count = c->proj_count;
+  hipError_t e = bg::launch_qkv_proj(view(c, layer), a, (hipStream_t)stream);
+  return e == hipSuccess ? BG_OK : hip_fail(e, "qkv projection launch");
 }
 
 int32_t bg_kv_evict(bg_kv_cache* c, int32_t fill, int32_t need, int32_t* new_fill) {

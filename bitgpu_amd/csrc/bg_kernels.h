@@ -49,6 +49,31 @@ struct PrologueArgs {
 };
 hipError_t launch_qkv_prologue(const LayerView& L, const PrologueArgs& a, hipStream_t st);
 
+// gemv.hip: 1-bit decode projections. Row n, weight k = bit k % 32 of sign[n][k / 32] (set =
+// +1) times scales[n][k / 128]; K a multiple of 128.
+struct GemvArgs {
+  const float* x; int K;
+  const uint32_t* sign; const float* scales;
+  int N0, N1, N2;                  // rows [0, N0) -> out0, [N0, N0+N1) -> out1, the rest -> out2
+  float* out0; float* out1; float* out2;
+  const float* resid;              // nullable: added to every output (the residual form)
+};
+hipError_t launch_gemv(const GemvArgs& a, hipStream_t st);
+// fused decode qkv projection + prologue over the rows of H query heads, then KV key and KV
+// value heads of the cache's head_dim
+struct QkvProjArgs {
+  const float* x; int K;
+  const uint32_t* sign; const float* scales;
+  int H;
+  const float* q_gamma; const float* k_gamma; float eps;
+  const float* cos_tab; const float* sin_tab; int rot_dim;
+  int pos, slot;
+  float* q_out;                    // [H, D]: raw rows first, then the normed, roped rows
+  float* kv_raw;                   // [2 KV D] raw K and V rows
+  unsigned* count;                 // [H + 2 KV] arrival counters, zero between launches
+};
+hipError_t launch_qkv_proj(const LayerView& L, const QkvProjArgs& a, hipStream_t st);
+
 // attention (decode.hip, attn_f32.hip, prefill.hip)
 struct AttnArgs {
   const float* q;

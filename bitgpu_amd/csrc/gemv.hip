@@ -1,0 +1,270 @@
+// 1-bit decode projections on either side of attention (M = 1 GEMVs over sign-bit weights).
+//
+// Replaces matmul_split_sg.wgsl (fusedMM: the qkv and gate/up projections, outputs routed to up
+// to three buffers by row range) and matmul_resid_mr_sg.wgsl (residMM: o_proj / down_proj with
+// the residual added), src/engine.ts:1344-1380, and fuses the decode attention prologue into
+// the qkv projection (src/engine.ts:1526-1540: matmul_split_sg, appendKV(V), rmsnorm_rope_sg(Q),
+// ROPE_K / rmsnorm_rope_sg_kv8(K)).
+//
+// Weights: row n, weight k is bit k % 32 of sign word [n][k / 32] (set = +1, clear = -1) times the
+// f32 scale [n][k / 128] (shaders/matmul_split_sg.wgsl:24-35).
+//
+//   rows    a wave computes kGemvRW output rows; a lane owns one 32-weight word of each row per
+//           2048-weight tile of K and the 32 x values under it (eight 16-byte loads, reused by the
+//           wave's rows). The word's signs flip the x values' sign bits (one xor each), four
+//           partial sums per word, times the word's block scale; a DPP / permlane wave sum
+//           finishes the row. Two tiles' loads (the rows' words and scales, x) are in flight:
+//           the next tile is issued before the current one's arithmetic; the residual is
+//           loaded at the start.
+//   fused   the qkv kernel's workgroups own 16 rows of one head; each stores its raw rows (Q
+//           into q_out, K and V into the cache's small raw buffer), and the last workgroup of a
+//           head to arrive (an arrival counter per head, reset by that workgroup) normalizes
+//           and ropes the head (Q -> q_out; K -> the cache row, unroped in sink mode) or stores
+//           it (V), with the fused prologue's row arithmetic (bg_qkrow.h).
+#include "bg_kernels.h"
+#include "bg_qkrow.h"
+
+namespace bg {
+
+constexpr int kGemvRW = 4;  // rows per wave
+
+// One 2048-weight tile of a wave's rows: the lane's sign word (word 64t + l) and block scale of
+// each row and the 32 x values under the word.
+template <int RW>
+struct GemvTile {
+  uint32_t word[RW];
+  float sc[RW];
+  float xv[32];
+};
+
+// x staged in LDS by the workgroup: word w's 32 values at float offset 36 w (4 floats of pad
+// per word keep the lanes' 16-byte reads of consecutive words on different banks)
+constexpr int kXPad = 36;
+constexpr int kGemvLdsMaxK = 12288;  // 54 KB of LDS; longer rows read x from global memory
+
+template <int RW>
+__device__ __forceinline__ void gemv_load_w(GemvTile<RW>& T, int W, int NB, const uint32_t* __restrict__ sign,
+                                            const float* __restrict__ scales, int n0, int n_rows, int t, int lane) {
+  const int w = 64 * t + lane;
+  const bool ok = w < W;
+#pragma unroll
+  for (int r = 0; r < RW; r++) {
+    const int n = n0 + r;
+    const bool v = ok && n < n_rows;
+    T.word[r] = v ? sign[(size_t)n * W + w] : 0u;
+    T.sc[r] = v ? scales[(size_t)n * NB + (w >> 2)] : 0.0f;
+  }
+}
+
+template <int RW, bool XLDS>
+__device__ __forceinline__ void gemv_load_x(GemvTile<RW>& T, const float* __restrict__ x, const float* xs, int W, int t,
+                                            int lane) {
+  const int w = 64 * t + lane;
+  const bool ok = w < W;
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    float4 f;
+    if constexpr (XLDS) f = ok ? *(const float4*)(xs + kXPad * w + 4 * j) : make_float4(0.f, 0.f, 0.f, 0.f);
+    else f = ok ? *(const float4*)(x + 32 * w + 4 * j) : make_float4(0.f, 0.f, 0.f, 0.f);
+    T.xv[4 * j] = f.x;
+    T.xv[4 * j + 1] = f.y;
+    T.xv[4 * j + 2] = f.z;
+    T.xv[4 * j + 3] = f.w;
+  }
+}
+
+template <int RW, bool XLDS>
+__device__ __forceinline__ void gemv_load(GemvTile<RW>& T, const float* __restrict__ x, const float* xs, int W, int NB,
+                                          const uint32_t* __restrict__ sign, const float* __restrict__ scales,
+                                          int n0, int n_rows, int t, int lane) {
+  gemv_load_w<RW>(T, W, NB, sign, scales, n0, n_rows, t, lane);
+  gemv_load_x<RW, XLDS>(T, x, xs, W, t, lane);
+}
+
+// stage x[K] into xs (the whole workgroup, coalesced 16-byte loads), then a barrier
+__device__ __forceinline__ void gemv_stage_x(const float* __restrict__ x, float* xs, int K) {
+  for (int i = threadIdx.x; i < K / 4; i += blockDim.x) {
+    const float4 f = *(const float4*)(x + 4 * i);
+    *(float4*)(xs + kXPad * (i >> 3) + 4 * (i & 7)) = f;
+  }
+  __syncthreads();
+}
+
+template <int RW>
+__device__ __forceinline__ void gemv_accumulate(const GemvTile<RW>& T, float (&acc)[RW], int lane) {
+  (void)lane;
+#pragma unroll
+  for (int r = 0; r < RW; r++) {
+    // clear bit i -> weight -1: flip the sign bit of x_i
+    const uint32_t nw = ~T.word[r];
+    float p[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < 32; i++) p[i & 3] += __uint_as_float(__float_as_uint(T.xv[i]) ^ ((nw << (31 - i)) & 0x80000000u));
+    acc[r] = fmaf((p[0] + p[1]) + (p[2] + p[3]), T.sc[r], acc[r]);
+  }
+}
+
+// totals of rows n0 .. n0 + RW - 1 (rows >= n_rows give 0); every lane holds every total. Two
+// tiles are in flight: the next tile's loads are issued before the current tile's arithmetic
+// (a uniform trip count, so the compiler keeps them outstanding across the loop head).
+// (the caller issues tile 0's weight loads into A, then stages x when XLDS, then calls this)
+template <int RW, bool XLDS>
+__device__ inline void gemv_rows(GemvTile<RW>& A, const float* __restrict__ x, const float* xs, int K,
+                                 const uint32_t* __restrict__ sign, const float* __restrict__ scales, int n0, int n_rows,
+                                 int lane, float (&tot)[RW]) {
+  const int W = K >> 5, NB = K >> 7;
+  const int n_tiles = (W + 63) >> 6;
+  float acc[RW];
+#pragma unroll
+  for (int r = 0; r < RW; r++) acc[r] = 0.0f;
+  GemvTile<RW> B;
+  gemv_load_x<RW, XLDS>(A, x, xs, W, 0, lane);
+  int t = 0;
+  for (; t + 2 <= n_tiles; t += 2) {
+    gemv_load<RW, XLDS>(B, x, xs, W, NB, sign, scales, n0, n_rows, t + 1, lane);
+    gemv_accumulate<RW>(A, acc, lane);
+    if (t + 2 < n_tiles) gemv_load<RW, XLDS>(A, x, xs, W, NB, sign, scales, n0, n_rows, t + 2, lane);
+    gemv_accumulate<RW>(B, acc, lane);
+  }
+  if (t < n_tiles) gemv_accumulate<RW>(A, acc, lane);
+#pragma unroll
+  for (int r = 0; r < RW; r++) tot[r] = wave_sum(acc[r]);
+}
+
+template <bool XLDS>
+__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
+  extern __shared__ __align__(16) float xs[];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int N = a.N0 + a.N1 + a.N2;
+  const int n0 = (blockIdx.x * 4 + wave) * kGemvRW;
+  // lane r < kGemvRW stores row n0 + r: its residual and the first tile's weights are loaded
+  // before x is staged
+  const float res = (a.resid && lane < kGemvRW && n0 + lane < N) ? a.resid[n0 + lane] : 0.0f;
+  GemvTile<kGemvRW> A;
+  gemv_load_w<kGemvRW>(A, a.K >> 5, a.K >> 7, a.sign, a.scales, n0, N, 0, lane);
+  if constexpr (XLDS) gemv_stage_x(a.x, xs, a.K);
+  if (n0 >= N) return;  // wave-uniform
+  float tot[kGemvRW];
+  gemv_rows<kGemvRW, XLDS>(A, a.x, xs, a.K, a.sign, a.scales, n0, N, lane, tot);
+#pragma unroll
+  for (int r = 0; r < kGemvRW; r++) {
+    const int n = n0 + r;
+    if (lane == r && n < N) {
+      const float y = a.resid ? tot[r] + res : tot[r];
+      if (n < a.N0) a.out0[n] = y;
+      else if (n < a.N0 + a.N1) a.out1[n - a.N0] = y;
+      else a.out2[n - a.N0 - a.N1] = y;
+    }
+  }
+}
+
+hipError_t launch_gemv(const GemvArgs& a, hipStream_t st) {
+  const int N = a.N0 + a.N1 + a.N2;
+  if (N <= 0) return hipSuccess;
+  const int waves = (N + kGemvRW - 1) / kGemvRW;
+  if (a.K <= kGemvLdsMaxK) {
+    const size_t lds = (size_t)(a.K / 32) * kXPad * sizeof(float);
+    hipLaunchKernelGGL(gemv_kernel<true>, dim3((waves + 3) / 4), dim3(256), lds, st, a);
+  } else {
+    hipLaunchKernelGGL(gemv_kernel<false>, dim3((waves + 3) / 4), dim3(256), 0, st, a);
+  }
+  return hipGetLastError();
+}
+
+// ---- fused decode qkv projection + prologue ---------------------------------------------------
+constexpr int kQkvRowsPerWg = 4 * kGemvRW;  // 16 rows of one head
+
+template <int D, int DT, bool XLDS>
+__global__ __launch_bounds__(256) void qkv_proj_kernel(LayerView L, QkvProjArgs a) {
+  constexpr int LPR = D / 4;  // lanes per row in the epilogue
+  extern __shared__ __align__(16) float xs[];
+  __shared__ __align__(16) float rrow[D];
+  __shared__ unsigned s_last;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int KV = L.kv_heads;
+  const int nq = a.H * D;
+  const int N = nq + 2 * KV * D;
+  const int wg_n0 = blockIdx.x * kQkvRowsPerWg;
+  const int head = wg_n0 / D;  // 0 .. H-1: Q heads, then K heads, then V heads
+  {
+    const int n0 = wg_n0 + wave * kGemvRW;
+    GemvTile<kGemvRW> A;
+    gemv_load_w<kGemvRW>(A, a.K >> 5, a.K >> 7, a.sign, a.scales, n0, N, 0, lane);
+    if constexpr (XLDS) gemv_stage_x(a.x, xs, a.K);
+    float tot[kGemvRW];
+    gemv_rows<kGemvRW, XLDS>(A, a.x, xs, a.K, a.sign, a.scales, n0, N, lane, tot);
+#pragma unroll
+    for (int r = 0; r < kGemvRW; r++) {
+      const int n = n0 + r;
+      if (lane == r) st_coherent(n < nq ? a.q_out + n : a.kv_raw + (n - nq), tot[r]);
+    }
+  }
+  wait_stores();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned prev = __hip_atomic_fetch_add(&a.count[head], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = prev == (unsigned)(D / kQkvRowsPerWg - 1) ? 1u : 0u;
+  }
+  __syncthreads();
+  if (!s_last || wave != 0) return;
+
+  // ---- the last workgroup of the head: one wave, 4 dims a lane (D=128: both halves of the
+  // wave hold the row; the lower one stores) ----
+  const int c = lane % LPR;
+  const bool writer = lane < LPR;
+  const bool isq = head < a.H, isk = !isq && head < a.H + KV;
+  const float* raw = isq ? a.q_out + head * D : a.kv_raw + (head - a.H) * D;
+  float x[4];
+#pragma unroll
+  for (int e = 0; e < 4; e++) x[e] = ld_coherent(raw + 4 * c + e);
+  if (isq || isk) {
+    float g[4];
+    load4((isq ? a.q_gamma : a.k_gamma) + 4 * c, g);
+    row_scale(x, row_inv_rms<D, LPR>(x, a.eps), g);
+    const bool rope = isq || !L.ring.roll;  // sink mode caches K unroped (src/engine.ts:1530-1533)
+    if (rope) {
+      if (writer) *(float4*)(rrow + 4 * c) = make_float4(x[0], x[1], x[2], x[3]);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      float cs[4], sn[4];
+      row_tables(a.cos_tab, a.sin_tab, a.pos, a.rot_dim, c, cs, sn);
+      row_rope(x, rrow, c, a.rot_dim, cs, sn);
+    }
+    if (isq) {
+      if (writer) *(float4*)(a.q_out + head * D + 4 * c) = make_float4(x[0], x[1], x[2], x[3]);
+    } else {
+      // every lane joins the q8 block maxima; the lower half stores
+      if (D == 256 || writer) store_k4<D, DT>(L, L.ring.phys(a.slot), head - a.H, x, c);
+    }
+  } else {
+    if (D == 256 || writer) store_v4<D, DT>(L, L.ring.phys(a.slot), head - a.H - KV, x, c);
+  }
+  if (lane == 0) __hip_atomic_store(&a.count[head], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int D, bool XLDS>
+static void launch_qkv_proj_d(const LayerView& L, const QkvProjArgs& a, dim3 g, size_t lds, hipStream_t st) {
+  switch (L.dtype) {
+    case KV_F32: hipLaunchKernelGGL((qkv_proj_kernel<D, KV_F32, XLDS>), g, dim3(256), lds, st, L, a); break;
+    case KV_F16: hipLaunchKernelGGL((qkv_proj_kernel<D, KV_F16, XLDS>), g, dim3(256), lds, st, L, a); break;
+    default: hipLaunchKernelGGL((qkv_proj_kernel<D, KV_Q8, XLDS>), g, dim3(256), lds, st, L, a); break;
+  }
+}
+
+hipError_t launch_qkv_proj(const LayerView& L, const QkvProjArgs& a, hipStream_t st) {
+  const int N = (a.H + 2 * L.kv_heads) * L.D;
+  const dim3 g(N / kQkvRowsPerWg);
+  const bool xlds = a.K <= kGemvLdsMaxK;
+  const size_t lds = xlds ? (size_t)(a.K / 32) * kXPad * sizeof(float) : 0;
+  if (L.D == 128) {
+    if (xlds) launch_qkv_proj_d<128, true>(L, a, g, lds, st);
+    else launch_qkv_proj_d<128, false>(L, a, g, lds, st);
+  } else {
+    if (xlds) launch_qkv_proj_d<256, true>(L, a, g, lds, st);
+    else launch_qkv_proj_d<256, false>(L, a, g, lds, st);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace bg

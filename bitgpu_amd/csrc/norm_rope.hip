@@ -23,6 +23,7 @@
 // (tools/reference.py:149-152; shaders/rmsnorm_rope_sg.wgsl:32), no FMA contraction. Inputs are
 // read once: nontemporal loads keep them from displacing lines the next kernel reuses.
 #include "bg_kernels.h"
+#include "bg_qkrow.h"
 #include "bg_store.h"
 
 namespace bg {
@@ -117,31 +118,6 @@ struct RowLayout {
   static constexpr int NI = 4;              // load instructions per item
   static constexpr int RB = RPI * NI;       // rows per wave item
 };
-
-// Store one K row (4 dims per lane, LPR lanes) in the storage format: f32 / f16 as one vector
-// store a lane, q8 as the lane's four codes in one word plus the block scale (32 dims = 8
-// lanes) from the block's first lane.
-template <int D, int DT>
-__device__ inline void store_k4(const LayerView& L, int slot, int kvh, const float (&y)[4], int c) {
-  const size_t off = k_offset(kvh, slot, 4 * c, L.cap, D);
-  if constexpr (DT == KV_Q8) {
-    float m = fmaxf(fmaxf(fabsf(y[0]), fabsf(y[1])), fmaxf(fabsf(y[2]), fabsf(y[3])));
-    m = group_max<kBlock / 4>(m);
-    const float sc = q8_scale_of(m);
-    if ((c % (kBlock / 4)) == 0) L.ks[scale_offset(kvh, slot, (4 * c) / kBlock, L.cap, D)] = sc;
-    uint32_t w = 0;
-#pragma unroll
-    for (int e = 0; e < 4; e++) w |= (uint32_t)(uint8_t)(int8_t)q8_code(y[e], sc) << (8 * e);
-    *(uint32_t*)((int8_t*)L.k + off) = w;
-  } else if constexpr (DT == KV_F16) {
-    union { __half h[4]; uint2 u; } o;
-#pragma unroll
-    for (int e = 0; e < 4; e++) o.h[e] = __float2half_rn(y[e]);
-    *(uint2*)((__half*)L.k + off) = o.u;
-  } else {
-    *(float4*)((float*)L.k + off) = make_float4(y[0], y[1], y[2], y[3]);
-  }
-}
 
 template <int D, int DT>
 __global__ __launch_bounds__(256) void qkv_prologue_kernel(LayerView L, PrologueArgs a, PrologueGrid gr) {
@@ -244,14 +220,7 @@ __global__ __launch_bounds__(256) void qkv_prologue_kernel(LayerView L, Prologue
     for (int i = 0; i < NI; i++) {
       const int r = item * RB + RPI * i + h;
       const bool isq = r < gr.nq;
-      float ss = 0.0f;
-#pragma unroll
-      for (int e = 0; e < 4; e++) ss = __fadd_rn(ss, __fmul_rn(x[i][e], x[i][e]));
-      ss = group_sum<LPR>(ss);
-      // ss / D is exact as a product: D is a power of two
-      const float inv = rsqrtf(__fadd_rn(ss * (1.0f / D), a.eps));
-#pragma unroll
-      for (int e = 0; e < 4; e++) x[i][e] = __fmul_rn(__fmul_rn(x[i][e], inv), isq ? gq[e] : gk[e]);
+      row_scale(x[i], row_inv_rms<D, LPR>(x[i], a.eps), isq ? gq : gk);
       *(float4*)(rb + (RPI * i + h) * D + 4 * c) = make_float4(x[i][0], x[i][1], x[i][2], x[i][3]);
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -263,17 +232,7 @@ __global__ __launch_bounds__(256) void qkv_prologue_kernel(LayerView L, Prologue
       const bool isq = r < gr.nq;
       // y*cos + rot*sin as two rounded products and a rounded sum (tools/reference.py:149-152;
       // shaders/rmsnorm_rope_sg.wgsl:32); rot = -x[d + half] below half, x[d - half] above
-      if ((isq || gr.rope_k) && 4 * c < rot) {
-        const float* row = rb + (RPI * i + h) * D;
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const int d = 4 * c + e;
-          if (d < rot) {
-            const float rv = d < half ? -row[d + half] : row[d - half];
-            x[i][e] = __fadd_rn(__fmul_rn(x[i][e], cs[i][e]), __fmul_rn(rv, sn[i][e]));
-          }
-        }
-      }
+      if (isq || gr.rope_k) row_rope(x[i], rb + (RPI * i + h) * D, c, rot, cs[i], sn[i]);
       if (r < nqk) {
         if (isq) {
           *(float4*)(a.q_out + (size_t)r * D + 4 * c) = make_float4(x[i][0], x[i][1], x[i][2], x[i][3]);

@@ -11,6 +11,9 @@ The reference (stfurkan/bitgpu v0.19.1, src/engine.ts) records, per layer:
                                                                -> :class:`KvCache` methods
   (restoreCache's checks, 2808-2845                           -> :func:`validate_snapshot`)
 * ``synthRope`` (117-147)                                      -> :func:`rope_tables`
+* ``fusedMM`` / ``residMM`` at S = 1 (1344-1380)                -> :func:`fused_mm` / :func:`resid_mm`
+* the fused decode block's qkv projection + prologue (1526-1540) -> :func:`qkv_proj_prologue`,
+  and the block through o_proj + residual (1519-1547)          -> :func:`decode_attention_block`
 
 Device memory is owned by torch tensors (``cuda`` device, float32, contiguous); only raw
 pointers cross the boundary. Every call is enqueued on torch's current stream. There is no CPU
@@ -27,7 +30,8 @@ from ._lib import (BG_E_INVALID, BG_E_STATE, BG_K, BG_KSCALE, BG_ROPE_ABSOLUTE, 
                    KV_DTYPES, BitgpuError, check, lib)
 
 __all__ = ["KvCache", "attention", "qkv_prologue", "layer_attention", "hybrid_full_attention",
-           "rope_tables", "evict_plan", "ring_map", "validate_snapshot"]
+           "rope_tables", "evict_plan", "ring_map", "validate_snapshot", "OneBitWeight", "fused_mm", "resid_mm",
+           "qkv_proj_prologue", "decode_attention_block"]
 
 
 def _stream():
@@ -373,3 +377,74 @@ def hybrid_full_attention(cache: KvCache, li: int, qg, k, v, S: int, H: int, pos
     check(lib().bg_attention(cache.handle, li, _ptr(qr), S, H, int(pos_base), scale,
                              C.c_void_p(qg.data_ptr() + D * 4), 2 * D, _ptr(out), _stream()))
     return out
+
+
+# --------------------------------------------------------------------------------------------
+# 1-bit projections on either side of attention (decode, M = 1)
+# --------------------------------------------------------------------------------------------
+class OneBitWeight:
+    """A 1-bit weight as the engine uploads it (GpuWeight, src/engine.ts:814-830): ``sign`` u32
+    [N, K/32] (bit k % 32 of word k // 32 set = +1), ``scales`` f32 [N, K/128], rows split into
+    ranges N0 | N1 | N2 for the fused qkv / gate-up weights (src/engine.ts:850-853)."""
+
+    def __init__(self, sign, scales, K: int, N0: int, N1: int = 0, N2: int = 0):
+        import torch
+        if sign.dtype != torch.int32 or scales.dtype != torch.float32:
+            raise TypeError("bitgpu_amd: sign must be int32 (raw u32 words) and scales float32")
+        if K % 128 or sign.numel() != (N0 + N1 + N2) * K // 32 or scales.numel() != (N0 + N1 + N2) * K // 128:
+            raise ValueError("bitgpu_amd: sign / scales do not match K and the row counts")
+        self.sign, self.scales, self.K, self.N0, self.N1, self.N2 = sign, scales, K, N0, N1, N2
+
+    @property
+    def N(self) -> int:
+        return self.N0 + self.N1 + self.N2
+
+
+def fused_mm(w: OneBitWeight, x, outs):
+    """fusedMM at S = 1 (src/engine.ts:1344-1350, matmul_split_sg.wgsl): rows of W x into up to
+    three outputs by range."""
+    _f32(x, "x")
+    o = list(outs) + [None] * (3 - len(outs))
+    check(lib().bg_gemv_split(_ptr(x), w.K, _ptr(w.sign), _ptr(w.scales), w.N0, w.N1, w.N2, _ptr(o[0]), _ptr(o[1]),
+                              _ptr(o[2]), _stream()))
+
+
+def resid_mm(w: OneBitWeight, x, resid, out=None):
+    """residMM at S = 1 (src/engine.ts:1364-1369, matmul_resid_mr_sg.wgsl): W x + resid."""
+    import torch
+    _f32(x, "x")
+    _f32(resid, "resid")
+    if out is None:
+        out = torch.empty(w.N, dtype=torch.float32, device=x.device)
+    check(lib().bg_gemv_resid(_ptr(x), w.K, _ptr(w.sign), _ptr(w.scales), w.N, _ptr(resid), _ptr(out), _stream()))
+    return out
+
+
+def qkv_proj_prologue(cache: KvCache, li: int, x, w_qkv: OneBitWeight, H: int, q_norm, k_norm, eps: float, cos_tab,
+                      sin_tab, rot_dim: int, pos: int, slot: int, q_out=None):
+    """The fused decode branch of ``layer()`` up to the attention (src/engine.ts:1526-1540): the
+    qkv projection of the normed hidden state x with Q norm + rope into q_out, K norm + rope into
+    the cache and V appended, in one launch. Returns q_out [1, H, D]."""
+    import torch
+    D = cache.head_dim
+    if w_qkv.N0 != H * D or w_qkv.N1 != cache.kv_heads * D or w_qkv.N2 != cache.kv_heads * D:
+        raise ValueError("bitgpu_amd: the qkv weight's row ranges must be H*D | KV*D | KV*D")
+    _f32(x, "x")
+    if q_out is None:
+        q_out = torch.empty((1, H, D), dtype=torch.float32, device=x.device)
+    check(lib().bg_qkv_proj_prologue(cache.handle, li, _ptr(x), w_qkv.K, _ptr(w_qkv.sign), _ptr(w_qkv.scales), H,
+                                     _ptr(q_norm), _ptr(k_norm), float(eps), _ptr(cos_tab), _ptr(sin_tab),
+                                     int(cos_tab.shape[0]), int(rot_dim), int(pos), int(slot), _ptr(q_out),
+                                     _stream()))
+    return q_out
+
+
+def decode_attention_block(cache: KvCache, li: int, n1, h, w_qkv: OneBitWeight, w_o: OneBitWeight, H: int, q_norm,
+                           k_norm, eps: float, cos_tab, sin_tab, pos: int, slot: int | None = None):
+    """The fused decode attention block of ``layer()`` (src/engine.ts:1519-1547): qkv projection
+    + prologue, attention at the slot, o_proj with the residual h. n1: the input-layernormed
+    hidden state [K]; returns h2 [hidden]."""
+    slot = pos if slot is None else slot
+    qr = qkv_proj_prologue(cache, li, n1, w_qkv, H, q_norm, k_norm, eps, cos_tab, sin_tab, cache.head_dim, pos, slot)
+    att = attention(cache, li, qr, 1, H, slot)
+    return resid_mm(w_o, att.reshape(-1), h)

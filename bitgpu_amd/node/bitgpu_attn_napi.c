@@ -226,6 +226,33 @@ static napi_value js_attention(napi_env env, napi_callback_info info) {
   return NULL;
 }
 
+/* gemvSplit(x, K, sign, scales, N0, N1, N2, out0, out1, out2, stream);
+   gemvResid(x, K, sign, scales, N, resid, y, stream);
+   qkvProjPrologue(cache, li, x, K, sign, scales, H, qGamma, kGamma, eps, cos, sin, ropePositions,
+                   rotDim, pos, slot, qOut, stream) -- device buffers as BigInt pointers */
+static napi_value js_gemv_split(napi_env env, napi_callback_info info) {
+  ARGS(11);
+  RC(bg_gemv_split(arg_ptr(env, a[0]), arg_i32(env, a[1]), arg_ptr(env, a[2]), arg_ptr(env, a[3]), arg_i32(env, a[4]),
+                   arg_i32(env, a[5]), arg_i32(env, a[6]), arg_ptr(env, a[7]), arg_ptr(env, a[8]), arg_ptr(env, a[9]),
+                   arg_ptr(env, a[10])));
+  return NULL;
+}
+static napi_value js_gemv_resid(napi_env env, napi_callback_info info) {
+  ARGS(8);
+  RC(bg_gemv_resid(arg_ptr(env, a[0]), arg_i32(env, a[1]), arg_ptr(env, a[2]), arg_ptr(env, a[3]), arg_i32(env, a[4]),
+                   arg_ptr(env, a[5]), arg_ptr(env, a[6]), arg_ptr(env, a[7])));
+  return NULL;
+}
+static napi_value js_qkv_proj_prologue(napi_env env, napi_callback_info info) {
+  ARGS(18);
+  RC(bg_qkv_proj_prologue(arg_cache(env, a[0]), arg_i32(env, a[1]), arg_ptr(env, a[2]), arg_i32(env, a[3]),
+                          arg_ptr(env, a[4]), arg_ptr(env, a[5]), arg_i32(env, a[6]), arg_ptr(env, a[7]),
+                          arg_ptr(env, a[8]), (float)arg_f64(env, a[9]), arg_ptr(env, a[10]), arg_ptr(env, a[11]),
+                          arg_i32(env, a[12]), arg_i32(env, a[13]), arg_i32(env, a[14]), arg_i32(env, a[15]),
+                          arg_ptr(env, a[16]), arg_ptr(env, a[17])));
+  return NULL;
+}
+
 static napi_value js_kv_evict(napi_env env, napi_callback_info info) {
   ARGS(3);
   int32_t nf;
@@ -374,6 +401,9 @@ static napi_value init(napi_env env, napi_value exports) {
       {"kvWrite", 0, js_kv_write, 0, 0, 0, napi_default, 0},
       {"qkvPrologue", 0, js_qkv_prologue, 0, 0, 0, napi_default, 0},
       {"attention", 0, js_attention, 0, 0, 0, napi_default, 0},
+      {"gemvSplit", 0, js_gemv_split, 0, 0, 0, napi_default, 0},
+      {"gemvResid", 0, js_gemv_resid, 0, 0, 0, napi_default, 0},
+      {"qkvProjPrologue", 0, js_qkv_proj_prologue, 0, 0, 0, napi_default, 0},
       {"kvEvict", 0, js_kv_evict, 0, 0, 0, napi_default, 0},
       {"kvEvictFor", 0, js_kv_evict_for, 0, 0, 0, napi_default, 0},
       {"kvRingState", 0, js_kv_ring_state, 0, 0, 0, napi_default, 0},

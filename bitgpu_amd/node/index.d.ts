@@ -25,7 +25,14 @@ export declare class KvCache {
   evictFor(fill: number, n: number): number
   exportRows(li: number, region: 0 | 1 | 2 | 3, base: number, count: number): ArrayBuffer
   importRows(li: number, region: 0 | 1 | 2 | 3, base: number, count: number, buf: ArrayBuffer): void
+  qkvProjPrologue(o: { li: number; x: DevPtr; w: OneBitWeight; H: number; qGamma: DevPtr; kGamma: DevPtr; eps: number;
+    cos: DevPtr; sin: DevPtr; ropePositions: number; rotDim: number; pos: number; slot?: number; qOut: DevPtr;
+    stream?: DevPtr | null }): void
 }
+// a 1-bit weight as the engine uploads it (GpuWeight, src/engine.ts:814-830)
+export interface OneBitWeight { sign: DevPtr; scales: DevPtr; K: number; N0: number; N1?: number; N2?: number; N?: number }
+export declare function fusedMM(w: OneBitWeight, x: DevPtr, outs: (DevPtr | null)[], stream?: DevPtr | null): void
+export declare function residMM(w: OneBitWeight, x: DevPtr, resid: DevPtr, out: DevPtr, stream?: DevPtr | null): void
 // raw addon: streams (default priority) and event timing, for hosts without a GPU runtime
 export declare const addon: {
   streamCreate(): DevPtr; streamDestroy(stream: DevPtr): void

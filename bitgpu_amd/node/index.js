@@ -11,6 +11,9 @@
 //   rmsnorm_rope_sg + ROPE_K + appendKV(v)          ->  cache.prologue({...})
 //   ensureKvCapacity / evict / evictFor             ->  cache.ensureKvCapacity / evict / evictFor
 //   synthRope                                       ->  synthRope(theta, rotDim, positions, yarn)
+//   fusedMM / residMM at S = 1 (1344-1380)          ->  fusedMM(w, x, outs) / residMM(w, x, resid, out)
+//   matmul_split_sg + rmsnorm_rope_sg + ROPE_K
+//     + appendKV(v), decode (1526-1540)             ->  cache.qkvProjPrologue({...})
 const path = require('path')
 const addon = require(path.join(__dirname, 'bitgpu_attn.node'))
 
@@ -75,6 +78,18 @@ class KvCache {
     return buf
   }
   importRows(li, region, base, count, buf) { call(() => addon.kvImportRows(this.h, li, region, base, count, buf, null)) }
+  // w = { sign, scales, K, N0, N1, N2 } (device pointers as BigInt, GpuWeight of src/engine.ts:814-830)
+  qkvProjPrologue({ li, x, w, H, qGamma, kGamma, eps, cos, sin, ropePositions, rotDim, pos, slot, qOut, stream = null }) {
+    call(() => addon.qkvProjPrologue(this.h, li, x, w.K, w.sign, w.scales, H, qGamma, kGamma, eps, cos, sin, ropePositions, rotDim, pos, slot === undefined ? pos : slot, qOut, stream))
+  }
 }
 
-module.exports = { addon, KvCache, synthRope, GpuOutOfMemoryError, K, V, KSCALE, VSCALE, KV_DTYPE }
+function fusedMM(w, x, outs, stream = null) {
+  call(() => addon.gemvSplit(x, w.K, w.sign, w.scales, w.N0, w.N1 || 0, w.N2 || 0, outs[0] || null, outs[1] || null, outs[2] || null, stream))
+}
+
+function residMM(w, x, resid, out, stream = null) {
+  call(() => addon.gemvResid(x, w.K, w.sign, w.scales, w.N || w.N0, resid, out, stream))
+}
+
+module.exports = { addon, KvCache, synthRope, fusedMM, residMM, GpuOutOfMemoryError, K, V, KSCALE, VSCALE, KV_DTYPE }

@@ -159,6 +159,38 @@ int32_t bg_qkv_prologue(bg_kv_cache* cache, int32_t layer, const float* q, int32
                         const float* cos_tab, const float* sin_tab, int32_t rope_positions,
                         int32_t rot_dim, int32_t pos0, int32_t slot0, float* q_out, void* stream);
 
+/* ---- 1-bit projections on either side of attention (decode, M = 1) -------------------------
+ * Weights as the engine uploads them (src/engine.ts:814-830): row n, weight k is bit k % 32 of
+ * sign[n][k / 32] (u32; set = +1, clear = -1) times scales[n][k / 128] (f32); K a multiple of
+ * 128; x, sign and scales 16-byte aligned. */
+
+/* fusedMM, matmul_split_sg.wgsl (src/engine.ts:1344-1360, e.g. the qkv and gate/up weights):
+ * the N0 + N1 + N2 rows of W x, rows [0, N0) to out0, [N0, N0+N1) to out1, the rest to out2. */
+int32_t bg_gemv_split(const float* x, int32_t K, const uint32_t* sign, const float* scales,
+                      int32_t N0, int32_t N1, int32_t N2, float* out0, float* out1, float* out2,
+                      void* stream);
+
+/* residMM, matmul_resid_mr_sg.wgsl (src/engine.ts:1364-1380, o_proj at 1547 and down_proj):
+ * y = W x + resid over N rows. */
+int32_t bg_gemv_resid(const float* x, int32_t K, const uint32_t* sign, const float* scales,
+                      int32_t N, const float* resid, float* y, void* stream);
+
+/* The decode qkv projection fused with the attention prologue, replacing src/engine.ts:1526-1540
+ * (matmul_split_sg into q, k, v; appendKV(V); rmsnorm_rope_sg(Q); ROPE_K / rmsnorm_rope_sg_kv8
+ * writing K into the cache): one token, x = the normed hidden state [K]. The weight's rows are
+ * the H query heads, then the cache's kv_heads key heads, then its value heads, head_dim rows
+ * each (the fused qkv weight of src/engine.ts:850). Q heads are RMSNormed with q_gamma and roped
+ * at `pos` into q_out [H, head_dim]; K heads normed with k_gamma, roped at `pos` (unroped in a
+ * sink-mode cache) and stored at logical slot `slot`; V heads stored at `slot`. Tables as in
+ * bg_qkv_prologue (16-byte aligned). H + 2 * kv_heads <= 1024. The arithmetic of the norm and
+ * the rotation is bg_qkv_prologue's: the result equals bg_gemv_split followed by
+ * bg_qkv_prologue bit for bit. */
+int32_t bg_qkv_proj_prologue(bg_kv_cache* cache, int32_t layer, const float* x, int32_t K,
+                             const uint32_t* sign, const float* scales, int32_t H,
+                             const float* q_gamma, const float* k_gamma, float eps,
+                             const float* cos_tab, const float* sin_tab, int32_t rope_positions,
+                             int32_t rot_dim, int32_t pos, int32_t slot, float* q_out, void* stream);
+
 /* ---- attention ---------------------------------------------------------------------------
  * runN(ATT, [S,H,KV,D,posBase,Ltot], attIns(qr, li), att, S*H), src/engine.ts:1543,1579-1580
  * (attention_{sg,wg}{,_kv16,_kv8}{,_roll}.wgsl) and the hybrid

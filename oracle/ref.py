@@ -29,6 +29,9 @@ Pinning (what fixes each function independently of its own formula; tests/test_o
 * ``f16_pack`` -- Python ``struct.pack('e')`` (IEEE round-to-nearest-even) on every tested value.
 * ``evict`` / ``evict_for`` / ``simulate_sink_schedule`` -- a literal row-by-row simulation of
   the reference's scratch-buffer memmove (src/engine.ts:1194-1210) on token ids.
+* ``unpack_signs`` / ``gemv_1bit`` -- one set bit at a time (the bit order), all-set / all-clear
+  rows (closed forms +-sum(x) * scale), and an explicit per-element loop that restates the WGSL
+  kernel's vec4 groups literally on small shapes.
 """
 from __future__ import annotations
 
@@ -299,3 +302,36 @@ def simulate_sink_schedule(prompt_len: int, target_abs: int, sinks: int, max_seq
         total += batch
     slot = do_evict(slot, final_rows)
     return cache[:slot], slot, events
+
+
+# --------------------------------------------------------------------------------------------
+# 1-bit projections (the GEMVs on either side of attention in decode)
+# --------------------------------------------------------------------------------------------
+def unpack_signs(sign: np.ndarray, K: int) -> np.ndarray:
+    """Sign bits ``u32[N, K/32]`` -> ``float64[N, K]`` of +-1: weight k of row n is bit k % 32 of
+    word k // 32, set = +1, clear = -1 (shaders/matmul_split_sg.wgsl:29-32)."""
+    s = np.asarray(sign, np.uint32)
+    N = s.shape[0]
+    bits = (s[:, :, None] >> np.arange(32, dtype=np.uint32)[None, None, :]) & np.uint32(1)
+    return np.where(bits.reshape(N, K) != 0, 1.0, -1.0)
+
+
+def gemv_1bit(x: np.ndarray, sign: np.ndarray, scales: np.ndarray, resid: np.ndarray | None = None) -> np.ndarray:
+    """``y[n] = sum_k x[k] * (+-1)[n, k] * scales[n, k // 128] (+ resid[n])`` in float64, returned
+    as float32: matmul_split_sg.wgsl:24-35 (qkv / gate-up, outputs split by range) and
+    matmul_resid_mr_sg.wgsl:24-46 (o_proj / down_proj with the residual added)."""
+    x = np.asarray(x, np.float64)
+    K = x.shape[-1]
+    w = unpack_signs(sign, K) * np.repeat(np.asarray(scales, np.float64), 128, axis=1)
+    y = w @ x
+    if resid is not None:
+        y = y + np.asarray(resid, np.float64)
+    return y.astype(f32)
+
+
+def gemv_abs_bound(x: np.ndarray, scales: np.ndarray) -> np.ndarray:
+    """``sum_k |x[k]| * scales[n, k // 128]``: the magnitude an f32 sum of the products of row n
+    is measured against (its rounding error is a small multiple of this times 2^-24)."""
+    xa = np.abs(np.asarray(x, np.float64))
+    K = xa.shape[-1]
+    return np.abs(np.asarray(scales, np.float64)) @ xa.reshape(K // 128, 128).sum(-1)

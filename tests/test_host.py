@@ -217,3 +217,16 @@ def test_decode_plan_residency_cap():
     assert rc == 0 and ns == 1 and nm == 0 and tps == tiles
     # shapes the decode kernel does not take
     assert _plan(8, 128, 64, 32, 1000)[0] == _lib.BG_E_UNSUPPORTED
+
+
+# ---------------------------------------------------------------- 1-bit projections: host checks
+def test_gemv_argument_validation():
+    lib = _lib.lib()
+    buf = (C.c_float * 64)()
+    p = C.cast(buf, C.c_void_p)
+    assert lib.bg_gemv_split(p, 100, p, p, 1, 0, 0, p, None, None, None) == _lib.BG_E_INVALID    # K % 128
+    assert b"multiple of 128" in lib.bg_last_error_message()
+    assert lib.bg_gemv_split(None, 128, p, p, 1, 0, 0, p, None, None, None) == _lib.BG_E_INVALID
+    assert lib.bg_gemv_split(p, 128, p, p, 1, 2, 0, p, None, None, None) == _lib.BG_E_INVALID    # out1 missing
+    assert lib.bg_gemv_resid(p, 128, p, p, 4, None, p, None) == _lib.BG_E_INVALID
+    assert lib.bg_qkv_proj_prologue(None, 0, p, 128, p, p, 8, p, p, 1e-6, p, p, 8, 128, 0, 0, p, None) == _lib.BG_E_INVALID

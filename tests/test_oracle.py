@@ -355,3 +355,52 @@ def test_sink_schedule_golden():
     s = np.array(slots)
     assert list(s[:4]) == [0, 1, 2, 3]                        # sinks never move
     assert np.all(np.diff(s[4:]) == 1) and s[-1] == 99_999    # the recent window is contiguous
+
+
+# ---------------------------------------------------------------- 1-bit projections
+def test_sign_bit_order_one_bit_at_a_time():
+    """Bit k % 32 of word k // 32 is weight k (shaders/matmul_split_sg.wgsl:29-32), set = +1."""
+    K = 256
+    for k in (0, 1, 31, 32, 77, 255):
+        sign = np.zeros((1, K // 32), np.uint32)
+        sign[0, k // 32] = np.uint32(1) << np.uint32(k % 32)
+        w = ref.unpack_signs(sign, K)[0]
+        assert w[k] == 1.0 and np.sum(w == 1.0) == 1 and np.sum(w == -1.0) == K - 1
+
+
+def test_gemv_closed_forms():
+    rng = np.random.default_rng(21)
+    K = 512
+    x = rng.standard_normal(K).astype(np.float32)
+    sc = np.abs(rng.standard_normal((2, K // 128))).astype(np.float32)
+    sign = np.zeros((2, K // 32), np.uint32)
+    sign[0] = 0xFFFFFFFF                                   # all +1
+    y = ref.gemv_1bit(x, sign, sc)
+    xb = x.astype(np.float64).reshape(K // 128, 128).sum(-1)
+    assert np.allclose(y[0], sc[0] @ xb, rtol=1e-6) and np.allclose(y[1], -(sc[1] @ xb), rtol=1e-6)
+    r = rng.standard_normal(2).astype(np.float32)
+    assert np.allclose(ref.gemv_1bit(x, sign, sc, r), y.astype(np.float64) + r, rtol=1e-6)
+
+
+def test_gemv_matches_wgsl_loop():
+    """Literal restatement of matmul_resid_mr_sg.wgsl's per-lane loop: vec4 groups, the 4 bits
+    at (word >> (k & 31)) & 0xf, dot times the block scale, then the cross-lane sum."""
+    rng = np.random.default_rng(22)
+    N, K, SG = 3, 384, 32
+    x = rng.standard_normal(K).astype(np.float32)
+    sign = rng.integers(0, 2 ** 32, (N, K // 32), dtype=np.uint64).astype(np.uint32)
+    sc = np.abs(rng.standard_normal((N, K // 128))).astype(np.float32)
+    resid = rng.standard_normal(N).astype(np.float32)
+    want = np.zeros(N)
+    for n in range(N):
+        lanes = []
+        for lane in range(SG):
+            acc = 0.0
+            for gi in range(lane, K // 4, SG):
+                k = gi * 4
+                bits4 = (int(sign[n, k >> 5]) >> (k & 31)) & 0xF
+                sv = [1.0 if (bits4 >> i) & 1 else -1.0 for i in range(4)]
+                acc += sum(float(x[k + i]) * sv[i] for i in range(4)) * float(sc[n, k // 128])
+            lanes.append(acc)
+        want[n] = sum(lanes) + float(resid[n])
+    assert np.allclose(ref.gemv_1bit(x, sign, sc, resid), want, rtol=1e-6, atol=1e-6)
