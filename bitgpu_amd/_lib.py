@@ -44,6 +44,7 @@ SIGNATURES = [
     ("bg_kv_destroy", _i32, [_vp]),
     ("bg_kv_capacity", _i32, [_vp, _pi32]),
     ("bg_kv_grow", _i32, [_vp, _i32, _vp]),
+    ("bg_kv_set_q8_block", _i32, [_vp, _i32]),
     ("bg_kv_set_rope", _i32, [_vp, _vp, _vp, _i32, _i32]),
     ("bg_kv_write", _i32, [_vp, _i32, _i32, _vp, _i32, _i32, _vp]),
     ("bg_qkv_prologue", _i32, [_vp, _i32, _vp, _i32, _vp, _vp, _i32, _i32, _vp, _vp, _f32,

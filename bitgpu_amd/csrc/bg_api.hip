@@ -39,6 +39,7 @@ struct bg_kv_cache {
   void* pf16 = nullptr;
   int pf16_cap = 0;
   int num_cus = 256;
+  int q8_row = 0;     // q8: one scale per row (bg_kv_set_q8_block with head_dim)
   // decode merge error word: pinned, coherent host memory the kernel writes when a merger's
   // bounded wait gives up (err_dev is its device address)
   unsigned* err_host = nullptr;
@@ -106,6 +107,7 @@ LayerView view(const bg_kv_cache* c, int layer) {
   L.rope_positions = c->rope_positions;
   L.rope_abs = c->rope_abs;
   L.evicted = c->evicted;
+  L.q8_row = c->q8_row;
   return L;
 }
 
@@ -483,6 +485,15 @@ int32_t bg_kv_grow(bg_kv_cache* c, int32_t needed, void* stream) {
   c->vs = nvs;
   c->capacity = newCap;
   c->cap = ncap;
+  return BG_OK;
+}
+
+int32_t bg_kv_set_q8_block(bg_kv_cache* c, int32_t block) {
+  if (!c) return fail(BG_E_INVALID, "bg_kv_set_q8_block: NULL cache");
+  if (c->dtype != BG_KV_Q8) return fail(BG_E_STATE, "bg_kv_set_q8_block: the cache is not q8");
+  if (block != 32 && block != c->D)
+    return fail(BG_E_UNSUPPORTED, "bg_kv_set_q8_block: block %d (32 or head_dim %d)", block, c->D);
+  c->q8_row = block == c->D && block != 32;
   return BG_OK;
 }
 

@@ -26,6 +26,8 @@ struct LayerView {
   int rope_positions;
   int rope_abs;       // 1: rotate by absolute position (slot + evicted for slots >= sinks)
   int64_t evicted;    // rows dropped by eviction so far
+  int q8_row;         // q8 writes: 1 = one scale per row (its maximum, stored in every 32-value
+                      // scale slot), 0 = one scale per 32 values
 };
 
 // kv_pack.hip

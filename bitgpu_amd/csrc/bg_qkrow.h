@@ -72,13 +72,14 @@ __device__ inline void load4(const float* p, float (&v)[4]) {
 
 // Store one K row (4 dims a lane, lanes c = 0 .. D/4-1) in the storage format: f32 / f16 as one
 // vector store a lane, q8 as the lane's four codes in one word plus the block scale (32 dims =
-// 8 lanes) from the block's first lane.
+// 8 lanes; in per-row mode the row maximum, in every block's slot) from the block's first lane.
 template <int D, int DT>
 __device__ inline void store_k4(const LayerView& L, int slot, int kvh, const float (&y)[4], int c) {
   const size_t off = k_offset(kvh, slot, 4 * c, L.cap, D);
   if constexpr (DT == KV_Q8) {
     float m = fmaxf(fmaxf(fabsf(y[0]), fabsf(y[1])), fmaxf(fabsf(y[2]), fabsf(y[3])));
     m = group_max<kBlock / 4>(m);
+    if (L.q8_row) m = group_max<D / 4>(m);
     const float sc = q8_scale_of(m);
     if ((c % (kBlock / 4)) == 0) L.ks[scale_offset(kvh, slot, (4 * c) / kBlock, L.cap, D)] = sc;
     uint32_t w = 0;
@@ -102,6 +103,7 @@ __device__ inline void store_v4(const LayerView& L, int slot, int kvh, const flo
   if constexpr (DT == KV_Q8) {
     float m = fmaxf(fmaxf(fabsf(y[0]), fabsf(y[1])), fmaxf(fabsf(y[2]), fabsf(y[3])));
     m = group_max<kBlock / 4>(m);
+    if (L.q8_row) m = group_max<D / 4>(m);
     const float sc = q8_scale_of(m);
     if ((c % (kBlock / 4)) == 0) L.vs[scale_offset(kvh, slot, (4 * c) / kBlock, L.cap, D)] = sc;
 #pragma unroll

@@ -17,6 +17,7 @@ __device__ inline void store_row(const LayerView& L, int which, int slot, int kv
 #pragma unroll
     for (int e = 0; e < EPL; e++) m = fmaxf(m, fabsf(v[e]));
     m = group_max<LPB>(m);
+    if (L.q8_row) m = wave_max(m);  // per-row scale: the row's 64 lanes
     const float s = q8_scale_of(m);
     float* sc = which == 0 ? L.ks : L.vs;
     if ((lane % LPB) == 0) sc[scale_offset(kvh, slot, d0 / kBlock, L.cap, D)] = s;

@@ -60,6 +60,7 @@ __device__ inline void store_vpanel(const LayerView& L, int kvh, int slot_base, 
 #pragma unroll
       for (int e = 0; e < EPL; e++) m = fmaxf(m, fabsf(v[i][e]));
       m = group_max<LPB>(m);
+      if (L.q8_row) m = wave_max(m);  // per-row scale: the row's 64 lanes
       sc[i] = q8_scale_of(m);
       if ((lane % LPB) == 0) L.vs[scale_offset(kvh, slot_base + vgroup_slot(B, i), d0 / kBlock, L.cap, D)] = sc[i];
     }

@@ -88,12 +88,13 @@ class KvCache:
     ``kv_cache`` is EngineOptions.kvCache ('f32' | 'f16' | 'q8'), ``overflow`` 'error' | 'sinks'
     and ``sink_tokens`` EngineOptions.sinkTokens (src/types.ts:138-177). ``rope_positions``
     selects the sink-mode key rotation: 'slot' (the reference's cache-relative positions) or
-    'absolute' (true token positions).
+    'absolute' (true token positions). ``q8_block`` is 32 (the reference's per-32 scales) or
+    head_dim (one scale per row, stored in every 32-value slot).
     """
 
     def __init__(self, n_layers: int, kv_heads: int, head_dim: int, kv_cache: str = "f32",
                  max_seq_len: int = 2048, capacity: int | None = None, overflow: str = "error",
-                 sink_tokens: int = 4, rope_positions: str = "slot"):
+                 sink_tokens: int = 4, rope_positions: str = "slot", q8_block: int = 32):
         if kv_cache not in KV_DTYPES:
             raise ValueError(f"bitgpu_amd: kvCache must be one of {sorted(KV_DTYPES)}")
         if overflow not in ("error", "sinks"):
@@ -108,6 +109,9 @@ class KvCache:
                                  0 if capacity is None else int(capacity), max_seq_len,
                                  1 if self.roll else 0, self.sinks, mode, C.byref(self._h)))
         self._rope_keepalive = None
+        self.q8_block = q8_block
+        if kv_cache == "q8" and q8_block != 32:
+            check(lib().bg_kv_set_q8_block(self._h, int(q8_block)))
 
     # -- lifecycle ---------------------------------------------------------------------------
     def close(self):

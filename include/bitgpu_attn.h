@@ -123,6 +123,13 @@ int32_t bg_kv_capacity(const bg_kv_cache* cache, int32_t* capacity);
  * buffers and BG_E_OOM is returned (the reference's rollback, 1157-1173). Synchronous. */
 int32_t bg_kv_grow(bg_kv_cache* cache, int32_t needed, void* stream);
 
+/* q8 scale block (src/types.ts:145-147: the reference quantizes per 32 values,
+ * shaders/copy_kv8.wgsl:30-36): 32 (the default) or head_dim, one scale per (position, kv head)
+ * row -- the row's maximum |value|, stored in each of the row's head_dim/32 scale slots, so the
+ * cache layout, the attention kernels and the snapshot format are the same in both modes.
+ * Applies to the writes that follow. BG_E_STATE for a cache that is not q8. */
+int32_t bg_kv_set_q8_block(bg_kv_cache* cache, int32_t block);
+
 /* Device rope tables [positions, rot_dim/2] used for the sink-mode read-time K rotation
  * (the rollCosT/rollSinT bindings of attIns, src/engine.ts:1097-1104,1395-1399). The caller
  * owns the buffers; they must cover max_seq_len positions (slot mode) or every absolute

@@ -250,3 +250,51 @@ def test_v2_snapshot_restores_into_a_wrapped_ring(dev, dtype):
         plain.restore_cache(snap)
     for c in (a, b, plain):
         c.close()
+
+
+@pytest.mark.parametrize("D", [128, 256])
+def test_q8_per_row_scale_mode(dev, D):
+    """q8 with one scale per (position, kv head) row (bg_kv_set_q8_block(head_dim)): appendKV and
+    the fused prologue store the codes of ref.q8_pack(x, block=D) bit for bit, the row scale in
+    each 32-value slot; decode and prefill attention over such a cache match the oracle."""
+    KV, H, L = 4, 16, 700
+    rng = np.random.default_rng(D + 1)
+    k = _rows(L, KV, D, 31)
+    v = _rows(L, KV, D, 32)
+    c = E.KvCache(1, KV, D, "q8", max_seq_len=1024, capacity=1024, q8_block=D)
+    fill_cache_raw(c, 0, k, v)
+    ek, ev, eks, evs = export_k_v(c, 0, 0, L)
+    for got, gs, x in ((ek, eks, k), (ev, evs, v)):
+        want, ws = ref.q8_pack(x, block=D)
+        assert np.array_equal(got, want)
+        assert np.array_equal(gs.view(np.uint32), np.repeat(ws, D // 32, -1).view(np.uint32))
+    # the fused prologue's K write (normed, roped) in per-row mode equals the quantizer on its f32
+    from tests.gpu_helpers import rope_dev
+    cos_d, sin_d, _, _ = rope_dev(1e6, D, 1024)
+    ones = t(np.ones(D, np.float32))
+    c32 = E.KvCache(1, KV, D, "f32", max_seq_len=1024, capacity=1024)
+    for cc in (c, c32):
+        E.qkv_prologue(cc, 0, None, t(k[:40]), t(v[:40]), 40, H, None, ones, 1e-6, cos_d, sin_d, D, 800, 800)
+    torch.cuda.synchronize()
+    k32, v32, _, _ = export_k_v(c32, 0, 800, 40)
+    kq, vq, ks, vs = export_k_v(c, 0, 800, 40)
+    for got, gs, x in ((kq, ks, k32), (vq, vs, v32)):
+        want, ws = ref.q8_pack(x, block=D)
+        assert np.array_equal(got, want) and np.array_equal(gs, np.repeat(ws, D // 32, -1))
+    c.close()
+    c32.close()
+    # attention reads it like any q8 cache (N(0,1) rows: the rows above span e^+-6 per row, whose
+    # scores are beyond the f16 query operand's resolution in any storage mode)
+    c = E.KvCache(1, KV, D, "q8", max_seq_len=1024, capacity=1024, q8_block=D)
+    k = rng.standard_normal((L, KV, D)).astype(np.float32)
+    v = rng.standard_normal((L, KV, D)).astype(np.float32)
+    fill_cache_raw(c, 0, k, v)
+    ek, ev, eks, evs = export_k_v(c, 0, 0, L)
+    assert np.array_equal(ek, ref.q8_pack(k, block=D)[0]) and np.array_equal(ev, ref.q8_pack(v, block=D)[0])
+    kk, vv = ref.q8_dequant(ek, eks), ref.q8_dequant(ev, evs)
+    for S in (1, 300):
+        q = rng.standard_normal((S, H, D)).astype(np.float32)
+        out = run_attention(c, 0, q, L - S)
+        exp = ref.attention(q, kk, vv, L - S)
+        assert np.abs(out - exp).max() / np.abs(exp).max() <= 2e-3
+    c.close()
