@@ -286,6 +286,13 @@ static napi_value js_kv_ring_reset(napi_env env, napi_callback_info info) {
   return NULL;
 }
 
+/* kvSetQ8Block(cache, block): q8 scale block, 32 or head_dim */
+static napi_value js_kv_set_q8_block(napi_env env, napi_callback_info info) {
+  ARGS(2);
+  RC(bg_kv_set_q8_block(arg_cache(env, a[0]), arg_i32(env, a[1])));
+  return NULL;
+}
+
 static napi_value js_kv_region_bytes(napi_env env, napi_callback_info info) {
   ARGS(3);
   size_t b;
@@ -408,6 +415,7 @@ static napi_value init(napi_env env, napi_value exports) {
       {"kvEvictFor", 0, js_kv_evict_for, 0, 0, 0, napi_default, 0},
       {"kvRingState", 0, js_kv_ring_state, 0, 0, 0, napi_default, 0},
       {"kvRingReset", 0, js_kv_ring_reset, 0, 0, 0, napi_default, 0},
+      {"kvSetQ8Block", 0, js_kv_set_q8_block, 0, 0, 0, napi_default, 0},
       {"kvRegionBytes", 0, js_kv_region_bytes, 0, 0, 0, napi_default, 0},
       {"kvExportRows", 0, js_kv_export, 0, 0, 0, napi_default, 0},
       {"kvImportRows", 0, js_kv_import, 0, 0, 0, napi_default, 0},

@@ -8,6 +8,7 @@ export interface KvCacheOptions {
   layers: number; kvHeads: number; headDim: number
   kvCache?: 'f32' | 'f16' | 'q8'; maxSeqLen?: number; capacity?: number
   overflow?: 'error' | 'sinks'; sinkTokens?: number; ropePositions?: 'slot' | 'absolute'
+  q8Block?: number   // q8 scale block: 32 (default, copy_kv8.wgsl) or headDim (one scale per row)
 }
 export declare class KvCache {
   constructor(opts: KvCacheOptions)
@@ -23,6 +24,8 @@ export declare class KvCache {
     o?: { scale?: number; gate?: DevPtr | null; gateStride?: number; stream?: DevPtr | null }): void
   evict(fill: number, need: number): number
   evictFor(fill: number, n: number): number
+  readonly ringState: [number, number]   // sink mode: [ring origin, rows evicted so far]
+  ringReset(evicted?: number): void      // compacted ring, the state a v2 snapshot restores into
   exportRows(li: number, region: 0 | 1 | 2 | 3, base: number, count: number): ArrayBuffer
   importRows(li: number, region: 0 | 1 | 2 | 3, base: number, count: number, buf: ArrayBuffer): void
   qkvProjPrologue(o: { li: number; x: DevPtr; w: OneBitWeight; H: number; qGamma: DevPtr; kGamma: DevPtr; eps: number;

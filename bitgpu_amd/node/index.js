@@ -51,14 +51,20 @@ function synthRope(theta, rotDim, positions, yarn) {
 
 class KvCache {
   // opts mirror EngineOptions (src/types.ts:138-177)
-  constructor({ layers, kvHeads, headDim, kvCache = 'f32', maxSeqLen = 2048, capacity = 0, overflow = 'error', sinkTokens = 4, ropePositions = 'slot' }) {
+  constructor({ layers, kvHeads, headDim, kvCache = 'f32', maxSeqLen = 2048, capacity = 0, overflow = 'error', sinkTokens = 4, ropePositions = 'slot', q8Block = 32 }) {
     const roll = overflow === 'sinks'
     this.kvHeads = kvHeads
     this.headDim = headDim
     this.kvCache = kvCache
     this.roll = roll
     this.h = call(() => addon.kvCreate(layers, kvHeads, headDim, KV_DTYPE[kvCache], capacity, maxSeqLen, roll ? 1 : 0, roll ? Math.max(1, Math.floor(sinkTokens)) : 0, ropePositions === 'absolute' ? 1 : 0))
+    // q8 scale block: 32 (copy_kv8.wgsl) or headDim (one scale per position and kv head)
+    if (kvCache === 'q8' && q8Block !== 32) call(() => addon.kvSetQ8Block(this.h, q8Block))
   }
+  // sink mode: [ring origin, rows evicted so far]; ringReset(evicted) compacts the ring (the
+  // state a v2 snapshot is restored into, restoreCache src/engine.ts:2807-2872)
+  get ringState() { return call(() => addon.kvRingState(this.h)) }
+  ringReset(evicted = 0) { call(() => addon.kvRingReset(this.h, evicted)) }
   dispose() { if (this.h) { addon.kvDestroy(this.h); this.h = null } }
   get capacity() { return addon.kvCapacity(this.h) }
   ensureKvCapacity(needed, stream = null) { call(() => addon.kvGrow(this.h, needed, stream)) }

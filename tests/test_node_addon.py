@@ -10,6 +10,7 @@ import numpy as np
 import pytest
 
 from bitgpu_amd import engine as E
+from bitgpu_amd._lib import BG_E_UNSUPPORTED
 from oracle import ref
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -89,3 +90,32 @@ console.log(JSON.stringify({{us}}))
     out = np.fromfile(tmp_path / "out.bin", np.float32).reshape(S, H, D)
     exp = ref.attention(q, ref.kv_roundtrip(k, dtype), ref.kv_roundtrip(v, dtype), L - S)
     assert np.abs(out - exp).max() / np.abs(exp).max() <= 2e-3
+
+
+@pytest.mark.gpu
+@pytestmark_node
+def test_addon_ring_state_and_q8_block(tmp_path):
+    """The shim's sink-mode ring state / reset (the compacted ring a v2 snapshot restores into)
+    and the q8 scale block option (32 or headDim; anything else is refused)."""
+    out = run_node("""
+const res = {}
+const c = new b.KvCache({layers: 1, kvHeads: 8, headDim: 128, kvCache: 'f16', maxSeqLen: 4100, overflow: 'sinks', sinkTokens: 4})
+res.s0 = c.ringState
+const fill = c.evictFor(4100, 4)
+res.fill = fill
+res.s1 = c.ringState
+c.ringReset(12345)
+res.s2 = c.ringState
+c.dispose()
+const q = new b.KvCache({layers: 1, kvHeads: 8, headDim: 128, kvCache: 'q8', maxSeqLen: 256, q8Block: 128})
+q.dispose()
+try { new b.KvCache({layers: 1, kvHeads: 8, headDim: 128, kvCache: 'q8', maxSeqLen: 256, q8Block: 64}) } catch (e) { res.err = [e.code, e.message] }
+console.log(JSON.stringify(res))
+""", tmp_path)
+    res = json.loads(out.strip().splitlines()[-1])
+    assert res["s0"] == [0, 0]
+    new_fill, dropped, _ = ref.evict_for(4100, 4, 4, 4100)
+    assert res["fill"] == new_fill and res["s1"][1] == dropped and res["s1"][0] == dropped % (4100 - 4)
+    assert res["s2"] == [0, 12345]
+    assert res["err"][0] == BG_E_UNSUPPORTED
+    assert "32 or head_dim 128" in res["err"][1]
