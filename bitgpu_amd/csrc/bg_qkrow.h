@@ -85,14 +85,14 @@ __device__ inline void store_k4(const LayerView& L, int slot, int kvh, const flo
     uint32_t w = 0;
 #pragma unroll
     for (int e = 0; e < 4; e++) w |= (uint32_t)(uint8_t)(int8_t)q8_code(y[e], sc) << (8 * e);
-    *(uint32_t*)((int8_t*)L.k + off) = w;
+    st_stream4((int8_t*)L.k + off, w);
   } else if constexpr (DT == KV_F16) {
     union { __half h[4]; uint2 u; } o;
 #pragma unroll
     for (int e = 0; e < 4; e++) o.h[e] = __float2half_rn(y[e]);
-    *(uint2*)((__half*)L.k + off) = o.u;
+    st_stream8((__half*)L.k + off, o.u.x, o.u.y);
   } else {
-    *(float4*)((float*)L.k + off) = make_float4(y[0], y[1], y[2], y[3]);
+    st_stream16f((float*)L.k + off, y[0], y[1], y[2], y[3]);
   }
 }
 

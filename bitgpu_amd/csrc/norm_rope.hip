@@ -70,7 +70,7 @@ __device__ inline void store_vpanel(const LayerView& L, int kvh, int slot_base, 
       uint32_t w[2] = {0u, 0u};
 #pragma unroll
       for (int i = 0; i < 8; i++) w[i >> 2] |= (uint32_t)(uint8_t)(int8_t)q8_code(v[i][e], sc[i]) << (8 * (i & 3));
-      *(uint2*)(base + 8 * e) = make_uint2(w[0], w[1]);
+      st_stream8(base + 8 * e, w[0], w[1]);
     }
   } else if constexpr (DT == KV_F16) {
     __half* base = (__half*)L.v + off0;
@@ -79,14 +79,14 @@ __device__ inline void store_vpanel(const LayerView& L, int kvh, int slot_base, 
       union { __half h[8]; uint4 u; } o;
 #pragma unroll
       for (int i = 0; i < 8; i++) o.h[i] = __float2half_rn(v[i][e]);
-      *(uint4*)(base + 8 * e) = o.u;
+      st_stream16(base + 8 * e, o.u.x, o.u.y, o.u.z, o.u.w);
     }
   } else {
     float* base = (float*)L.v + off0;
 #pragma unroll
     for (int e = 0; e < EPL; e++) {
-      *(float4*)(base + 8 * e) = make_float4(v[0][e], v[1][e], v[2][e], v[3][e]);
-      *(float4*)(base + 8 * e + 4) = make_float4(v[4][e], v[5][e], v[6][e], v[7][e]);
+      st_stream16f(base + 8 * e, v[0][e], v[1][e], v[2][e], v[3][e]);
+      st_stream16f(base + 8 * e + 4, v[4][e], v[5][e], v[6][e], v[7][e]);
     }
   }
 }
@@ -120,7 +120,9 @@ struct RowLayout {
   static constexpr int RB = RPI * NI;       // rows per wave item
 };
 
-template <int D, int DT>
+// SP: every batch of RB rows shares one position (H and KV multiples of RB), so a wave loads one
+// cos/sin row and holds it once (fewer registers: 8 waves a SIMD instead of 6)
+template <int D, int DT, bool SP>
 __global__ __launch_bounds__(256) void qkv_prologue_kernel(LayerView L, PrologueArgs a, PrologueGrid gr) {
   using RL = RowLayout<D>;
   constexpr int EPL = D / 64;
@@ -163,8 +165,9 @@ __global__ __launch_bounds__(256) void qkv_prologue_kernel(LayerView L, Prologue
     // one table row serves the whole batch when its rows share a position (every batch of a
     // Q or K range whose head count is a multiple of the batch)
     const int rf = item * RB, rl = min(item * RB + RB - 1, nqk - 1);
-    const bool same_pos = rl < gr.nq ? rf / a.H == rl / a.H : (rf >= gr.nq && (rf - gr.nq) / KV == (rl - gr.nq) / KV);
-    float x[NI][4], cs[NI][4], sn[NI][4];
+    const bool same_pos = SP || (rl < gr.nq ? rf / a.H == rl / a.H : (rf >= gr.nq && (rf - gr.nq) / KV == (rl - gr.nq) / KV));
+    constexpr int NT = SP ? 1 : NI;  // table rows held
+    float x[NI][4], cs[NT][4], sn[NT][4];
 #pragma unroll
     for (int i = 0; i < NI; i++) {
       const int r = min(item * RB + RPI * i + h, nqk - 1);  // past the end: recompute the last row, not stored
@@ -181,10 +184,12 @@ __global__ __launch_bounds__(256) void qkv_prologue_kernel(LayerView L, Prologue
       const float4 v4 = ld_stream4(src + 4 * c);
       x[i][0] = v4.x; x[i][1] = v4.y; x[i][2] = v4.z; x[i][3] = v4.w;
       if (i > 0 && same_pos) {
+        if constexpr (!SP) {
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-          cs[i][e] = cs[0][e];
-          sn[i][e] = sn[0][e];
+          for (int e = 0; e < 4; e++) {
+            cs[i < NT ? i : 0][e] = cs[0][e];
+            sn[i < NT ? i : 0][e] = sn[0][e];
+          }
         }
         continue;
       }
@@ -194,16 +199,17 @@ __global__ __launch_bounds__(256) void qkv_prologue_kernel(LayerView L, Prologue
       if (on && vec_tab) {
         const int ti = 4 * c < half ? 4 * c : 4 * c - half;
         const float4 c4 = *(const float4*)(a.cos_tab + prow + ti), s4 = *(const float4*)(a.sin_tab + prow + ti);
-        cs[i][0] = c4.x; cs[i][1] = c4.y; cs[i][2] = c4.z; cs[i][3] = c4.w;
-        sn[i][0] = s4.x; sn[i][1] = s4.y; sn[i][2] = s4.z; sn[i][3] = s4.w;
+        const int ti2 = i < NT ? i : 0;
+        cs[ti2][0] = c4.x; cs[ti2][1] = c4.y; cs[ti2][2] = c4.z; cs[ti2][3] = c4.w;
+        sn[ti2][0] = s4.x; sn[ti2][1] = s4.y; sn[ti2][2] = s4.z; sn[ti2][3] = s4.w;
       } else {
 #pragma unroll
         for (int e = 0; e < 4; e++) {
           const int d = 4 * c + e;
           const int ti = d < half ? d : d - half;
           const bool one = on && d < rot;
-          cs[i][e] = one ? a.cos_tab[prow + ti] : 0.0f;
-          sn[i][e] = one ? a.sin_tab[prow + ti] : 0.0f;
+          cs[i < NT ? i : 0][e] = one ? a.cos_tab[prow + ti] : 0.0f;
+          sn[i < NT ? i : 0][e] = one ? a.sin_tab[prow + ti] : 0.0f;
         }
       }
     }
@@ -233,10 +239,10 @@ __global__ __launch_bounds__(256) void qkv_prologue_kernel(LayerView L, Prologue
       const bool isq = r < gr.nq;
       // y*cos + rot*sin as two rounded products and a rounded sum (tools/reference.py:149-152;
       // shaders/rmsnorm_rope_sg.wgsl:32); rot = -x[d + half] below half, x[d - half] above
-      if (isq || gr.rope_k) row_rope(x[i], rb + (RPI * i + h) * D, c, rot, cs[i], sn[i]);
+      if (isq || gr.rope_k) row_rope(x[i], rb + (RPI * i + h) * D, c, rot, cs[i < NT ? i : 0], sn[i < NT ? i : 0]);
       if (r < nqk) {
         if (isq) {
-          *(float4*)(a.q_out + (size_t)r * D + 4 * c) = make_float4(x[i][0], x[i][1], x[i][2], x[i][3]);
+          st_stream16f(a.q_out + (size_t)r * D + 4 * c, x[i][0], x[i][1], x[i][2], x[i][3]);
         } else {
           const int rk = r - gr.nq;
           store_k4<D, DT>(L, L.ring.phys(a.slot0 + rk / KV), rk % KV, x[i], c);
@@ -297,10 +303,21 @@ static hipError_t prologue_d(const LayerView& L, const PrologueArgs& a, hipStrea
   const long items = ((long)gr.nq + gr.nk + RowLayout<D>::RB - 1) / RowLayout<D>::RB + (long)(gr.nvs + gr.ng) * L.kv_heads;
   if (items == 0) return hipSuccess;
   dim3 g((unsigned)((items + 3) / 4)), b(256);  // one item per wave
+  constexpr int RB = RowLayout<D>::RB;
+  const bool sp = (gr.nq == 0 || a.H % RB == 0) && (gr.nk == 0 || L.kv_heads % RB == 0);
   switch (L.dtype) {
-    case KV_F32: hipLaunchKernelGGL((qkv_prologue_kernel<D, KV_F32>), g, b, 0, st, L, a, gr); break;
-    case KV_F16: hipLaunchKernelGGL((qkv_prologue_kernel<D, KV_F16>), g, b, 0, st, L, a, gr); break;
-    default: hipLaunchKernelGGL((qkv_prologue_kernel<D, KV_Q8>), g, b, 0, st, L, a, gr); break;
+    case KV_F32:
+      if (sp) hipLaunchKernelGGL((qkv_prologue_kernel<D, KV_F32, true>), g, b, 0, st, L, a, gr);
+      else hipLaunchKernelGGL((qkv_prologue_kernel<D, KV_F32, false>), g, b, 0, st, L, a, gr);
+      break;
+    case KV_F16:
+      if (sp) hipLaunchKernelGGL((qkv_prologue_kernel<D, KV_F16, true>), g, b, 0, st, L, a, gr);
+      else hipLaunchKernelGGL((qkv_prologue_kernel<D, KV_F16, false>), g, b, 0, st, L, a, gr);
+      break;
+    default:
+      if (sp) hipLaunchKernelGGL((qkv_prologue_kernel<D, KV_Q8, true>), g, b, 0, st, L, a, gr);
+      else hipLaunchKernelGGL((qkv_prologue_kernel<D, KV_Q8, false>), g, b, 0, st, L, a, gr);
+      break;
   }
   return hipGetLastError();
 }
