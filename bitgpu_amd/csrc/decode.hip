@@ -290,6 +290,15 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
       qv[i][0] = a.x; qv[i][1] = a.y; qv[i][2] = a.z; qv[i][3] = a.w;
       qv[i][4] = b.x; qv[i][5] = b.y; qv[i][6] = b.z; qv[i][7] = b.w;
     }
+    // The first tile is issued once q has arrived (q issued alone returns in ~0.3 us, while
+    // behind every CU's first tile, ~19 MB queued at once, it returns only after them), and the
+    // hi/lo conversion below runs while the tile streams in. The scheduling barriers keep the
+    // compiler from moving the tile loads above the wait or below the conversion.
+    __builtin_amdgcn_s_waitcnt(0xf70);  // vmcnt(0): q has arrived
+    __builtin_amdgcn_sched_barrier(0);
+    const int ta = tile0 < t_end ? tile0 : t_end - 1;
+    load_tile<D, DT, QUARTER>(A, ta * 32, g, n, kbase, vbase, ksb, vsb);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < QMAX; i++) {
       const int idx = i * NTHR + tid;
@@ -307,12 +316,6 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
       qs[o0] = hi.u;
       qs[o1] = lo.u;
     }
-    // The first tile is issued only once q has arrived: q issued alone returns in ~0.3 us, while
-    // behind every CU's first tile (~19 MB queued at once) it returns only after them. The
-    // scheduling barrier keeps the compiler from hoisting the tile loads above the q stores.
-    __builtin_amdgcn_sched_barrier(0);
-    const int ta = tile0 < t_end ? tile0 : t_end - 1;
-    load_tile<D, DT, QUARTER>(A, ta * 32, g, n, kbase, vbase, ksb, vsb);
   }
   // zero this wave's P tiles (rows never written stay zero) and set corr = 1
   {
