@@ -32,7 +32,7 @@ MFMA_F16_PEAK_TFLOPS = 2516.6  # MI355X dense fp16/bf16 MFMA
 
 def c3_bytes(L, KV=8, D=128, H=32):
     """Algorithmic bytes of one decode-attention layer over a q8 cache: K and V codes plus one
-    f32 scale per 32 values, and the f32 query and output (BASELINE.md section 3)."""
+    f32 scale per 32 values, and the f32 query and output."""
     return L * KV * 2 * (D + 4 * D // 32) + 2 * H * D * 4
 
 

@@ -39,7 +39,7 @@ C5 = Config("C5 Qwen3.5 gated hybrid q8", H=24, KV=4, D=256, kv="q8", theta=1e7,
 
 CONFIGS = {"C1": C1, "C2": C2, "C3": C3, "C4": C4, "C5": C5}
 
-# headline sizes
+# headline sizes (the benchmark configurations of BASELINE.json)
 C1_PAST = 512          # cached positions before the decode step at position 512
 C2_S = 2048            # prefill tokens
 C3_CONTEXTS = (4096, 16384, 32768)

@@ -1,8 +1,8 @@
 """GPU: attention parity against the oracle (tools/reference.py:158-175 and
 tools/qwen35_numpy.py:102-115 restated in oracle/ref.py) for every storage mode and kernel
-(exact-f32, split-K MFMA decode/verify, MFMA prefill), at the BASELINE configs' full sizes.
+(exact-f32, split-K MFMA decode/verify, MFMA prefill), at the benchmark configurations' full sizes.
 
-Tolerances: f32 KV max-abs <= 1e-4; f16 / q8 KV relative
+Tolerances (the benchmark's stated bar): f32 KV max-abs <= 1e-4; f16 / q8 KV relative
 max|delta| / max|ref| <= 2e-3, the oracle reading the same stored values the kernel reads
 (quantization error is not kernel error). The reference's own kernel case additionally keeps
 its bar max|delta| < 2e-3 and cosine > 0.99999 (scripts/verify-kernels.mjs:104)."""

@@ -12,7 +12,7 @@ things against the oracle run on the same raw draws:
   1e-3 of them) and scales to 4e-6; V (never transformed) bit-exact;
 * the attention output against ``ref.attention`` / ``ref.gated_attention`` over the oracle's own
   stored values (``kv_roundtrip``): max-abs 1e-4 for f32, relative 2e-3 and cosine > 0.99999 for
-  f16 / q8 (the BASELINE north-star tolerances).
+  f16 / q8 (the benchmark's stated tolerances).
 
 Configurations: C2 (S=2048 prefill, positions to 2047), C3 (32k decode, positions to 32767),
 C4 (sinks at absolute position 100000, slot and absolute RoPE, decode, 5-row verify and a

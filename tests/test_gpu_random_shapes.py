@@ -5,7 +5,7 @@ rest of the space the C ABI accepts: GQA ratios 1-16 (including the odd 3, 5, 7 
 do not fill a 32-row MFMA tile), 1-8 kv heads, head_dim 128 / 256, cached lengths that are not
 tile multiples, decode (1 row), verify (2-5 rows) and prefill (up to 300 rows) of every storage
 mode, with and without the output gate. Attention is compared with ``ref.attention`` /
-``ref.gated_attention`` over the values the cache holds (the BASELINE tolerances: f32 max-abs
+``ref.gated_attention`` over the values the cache holds (the benchmark's stated tolerances: f32 max-abs
 1e-4, f16 / q8 relative 2e-3 and cosine > 0.99999); the fused prologue with ``ref.norm_rope`` at a
 random position and rotary width (rtol / atol 4e-6)."""
 import numpy as np
