@@ -328,6 +328,15 @@ int32_t bg_kv_create(int32_t n_layers, int32_t kv_heads, int32_t head_dim, int32
     return fail(BG_E_INVALID, "bg_kv_create: unknown kv dtype %d", dtype);
   if (dtype == BG_KV_Q8 && head_dim % 32 != 0)  // src/engine.ts:372-373
     return fail(BG_E_INVALID, "kvCache 'q8' needs head_dim divisible by 32 (got %d)", head_dim);
+  {
+    // one kv head's K (or V) region, and the f16 prefill copy of a q8 layer, are addressed with
+    // 32-bit byte offsets by the buffer loads of the prefill kernel
+    const long long eb = dtype == BG_KV_F32 ? 4 : 2;
+    const long long per_head = (((long long)max_seq_len + 31) & ~31LL) * head_dim * eb;
+    if (per_head > 0x7fffffffLL)
+      return fail(BG_E_UNSUPPORTED, "bg_kv_create: max_seq_len %d x head_dim %d needs %lld bytes per kv head and layer, "
+                                    "beyond the 2^31 - 1 a kernel addresses", max_seq_len, head_dim, per_head);
+  }
   if (roll) {
     if (sinks < 1) return fail(BG_E_INVALID, "bg_kv_create: sink mode needs sinks >= 1 (got %d)", sinks);
     if (max_seq_len < sinks + 64)  // src/engine.ts:311-312

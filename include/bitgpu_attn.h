@@ -109,7 +109,11 @@ int32_t bg_event_destroy(void* event);
 
 /* ---- KV cache lifecycle ------------------------------------------------------------------
  * Replaces the Kc/Vc/Ksc/Vsc allocation of src/engine.ts:1044-1079, the kvCache/overflow/
- * sinkTokens/maxSeqLen options (src/types.ts:138-177) and the roll statics (1094-1111). */
+ * sinkTokens/maxSeqLen options (src/types.ts:138-177) and the roll statics (1094-1111).
+ * One kv head's K (or V) region of one layer must stay below 2^31 bytes (f32: 4 bytes a value,
+ * f16 and q8 2, counting a q8 layer's f16 prefill copy): max_seq_len x head_dim x that at most
+ * 2^31 - 1 after rounding up to 32 positions, e.g. at most 4,194,272 positions of f16 at head_dim
+ * 256; a larger one is BG_E_UNSUPPORTED. */
 int32_t bg_kv_create(int32_t n_layers, int32_t kv_heads, int32_t head_dim, int32_t dtype,
                      int32_t capacity, int32_t max_seq_len, int32_t roll, int32_t sinks,
                      int32_t rope_pos_mode, bg_kv_cache** out);

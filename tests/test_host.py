@@ -48,6 +48,9 @@ def test_version_and_error_message():
     ((1, 8, 128, 7, 0, 1024, 0, 0, 0), _lib.BG_E_INVALID),          # unknown dtype
     ((1, 8, 128, 1, 0, 100, 1, 40, 0), _lib.BG_E_INVALID),          # sinks + 64 > maxSeqLen
     ((1, 8, 128, 1, 0, 1024, 1, 0, 0), _lib.BG_E_INVALID),          # sink mode without sinks
+    ((1, 1, 256, 1, 0, 4194305, 0, 0, 0), _lib.BG_E_UNSUPPORTED),   # f16 kv head region >= 2^31 bytes
+    ((1, 1, 256, 0, 0, 2097153, 0, 0, 0), _lib.BG_E_UNSUPPORTED),   # f32 kv head region >= 2^31 bytes
+    ((1, 1, 128, 2, 0, 2**31 - 1, 0, 0, 0), _lib.BG_E_UNSUPPORTED), # q8 (its f16 prefill copy), no int overflow
 ])
 def test_create_validation(args, code):
     h = C.c_void_p()
