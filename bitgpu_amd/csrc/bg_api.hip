@@ -553,7 +553,7 @@ int32_t bg_qkv_prologue(bg_kv_cache* c, int32_t layer, const float* q, int32_t q
                          (uintptr_t)k_gamma | (uintptr_t)cos_tab | (uintptr_t)sin_tab) & 15;
   if (mis || (q && (q_stride & 3)))
     return fail(BG_E_INVALID, "bg_qkv_prologue: buffers must be 16-byte aligned and q_stride a multiple of 4");
-  if ((k || v) && (slot0 < 0 || slot0 + S > addressable(c)))
+  if ((k || v) && (slot0 < 0 || (long)slot0 + S > addressable(c)))
     return fail(BG_E_INVALID, "bg_qkv_prologue: slots %d..%d beyond capacity %d", slot0, slot0 + S - 1, addressable(c));
   bg::PrologueArgs a;
   a.q = q;
@@ -940,7 +940,7 @@ static int32_t transfer(bg_kv_cache* c, int32_t layer, int32_t region, int32_t b
   if (rc != BG_OK) return rc;
   if (!host && count > 0) return fail(BG_E_INVALID, "snapshot transfer: NULL host buffer");
   if (layer < 0 || layer >= c->n_layers) return fail(BG_E_INVALID, "snapshot transfer: layer %d out of range", layer);
-  if (base < 0 || base + count > addressable(c))
+  if (base < 0 || (long)base + count > addressable(c))
     return fail(BG_E_INVALID, "snapshot transfer: positions %d..%d beyond capacity %d", base, base + count - 1, addressable(c));
   if (count == 0) return BG_OK;
   hipStream_t st = (hipStream_t)stream;
