@@ -37,6 +37,7 @@ struct bg_kv_cache {
   size_t ws_counters = 0;
   // f16 copy of one q8 layer's attended slots for long prefills (K then V, cap_copy slots each)
   void* pf16 = nullptr;
+  float* pf_ml = nullptr;  // split-K prefill (m, l), bg::prefill_split_ml_bytes() once allocated
   int pf16_cap = 0;
   int num_cus = 256;
   int q8_row = 0;     // q8: one scale per row (bg_kv_set_q8_block with head_dim)
@@ -131,8 +132,11 @@ int addressable(const bg_kv_cache* c) { return c->roll ? c->max_seq : c->capacit
 // the array's name to a kernel (on the host it is a stand-in, not a device address): the device
 // address comes from hipGetSymbolAddress, once per device, and only that pointer is used.
 // Between launches every slot holds the decode kernel's empty marker; the set-up fills it once.
-constexpr size_t kScratchBytes = (size_t)8 << 20;  // 8 MiB per GPU
-__device__ __align__(256) unsigned char scratch[kScratchBytes];
+// Layout: the first kScratchBytes hold split partials (decode, split-K prefill) and the empty
+// marker between launches; the kScratchMlBytes after them hold a split-K prefill's (m, l) values.
+constexpr size_t kScratchBytes = (size_t)8 << 20;     // 8 MiB per GPU
+constexpr size_t kScratchMlBytes = (size_t)256 << 10;  // 256 KiB
+__device__ __align__(256) unsigned char scratch[kScratchBytes + kScratchMlBytes];
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices] = {};
@@ -422,6 +426,7 @@ int32_t bg_kv_destroy(bg_kv_cache* c) {
   if (c->ws) (void)hipFree(c->ws);
   if (c->ws_count) (void)hipFree(c->ws_count);
   if (c->pf16) (void)hipFree(c->pf16);
+  if (c->pf_ml) (void)hipFree(c->pf_ml);
   delete c;
   return BG_OK;
 }
@@ -575,13 +580,12 @@ int32_t bg_qkv_prologue(bg_kv_cache* c, int32_t layer, const float* q, int32_t q
   return e == hipSuccess ? BG_OK : hip_fail(e, "prologue launch");
 }
 
-static int32_t ensure_workspace(bg_kv_cache* c, int S, int H) {
-  size_t counters = 0;
-  size_t need = bg::decode_workspace_floats(view(c, 0), S, H, c->num_cus, &counters);
-  if (c->dtype == BG_KV_F32) {
-    const size_t f = bg::f32_workspace_floats(view(c, 0), S, H);
-    need = f > need ? f : need;
-  }
+// The attention workspace: decode split partials, f32 split partials or split-K prefill partials
+// (each launch uses one kind; every slot holds the empty marker between launches). Grows to at
+// least `need` floats and `counters` counters, keeping the larger of old and new.
+static int32_t ensure_workspace_floats(bg_kv_cache* c, size_t need, size_t counters) {
+  if (need < c->ws_floats) need = c->ws_floats;
+  if (counters < c->ws_counters) counters = c->ws_counters;
   if (need <= c->ws_floats && counters <= c->ws_counters) return BG_OK;
   if (c->ws) (void)hipFree(c->ws);
   if (c->ws_count) (void)hipFree(c->ws_count);
@@ -590,8 +594,8 @@ static int32_t ensure_workspace(bg_kv_cache* c, int S, int H) {
   c->ws_floats = 0;
   c->ws_counters = 0;
   hipError_t e = hipMalloc((void**)&c->ws, need * sizeof(float));
-  if (e == hipSuccess) e = hipMalloc((void**)&c->ws_count, counters * sizeof(unsigned));
-  if (e == hipSuccess) e = hipMemset(c->ws_count, 0, counters * sizeof(unsigned));
+  if (e == hipSuccess && counters) e = hipMalloc((void**)&c->ws_count, counters * sizeof(unsigned));
+  if (e == hipSuccess && counters) e = hipMemset(c->ws_count, 0, counters * sizeof(unsigned));
   // decode split slots start out "empty"; every decode launch leaves them that way
   if (e == hipSuccess) e = hipMemsetD32((hipDeviceptr_t)c->ws, (int)bg::decode_workspace_empty(), need);
   if (e == hipSuccess) e = hipDeviceSynchronize();
@@ -605,6 +609,28 @@ static int32_t ensure_workspace(bg_kv_cache* c, int S, int H) {
   c->ws_floats = need;
   c->ws_counters = counters;
   return BG_OK;
+}
+
+// split-K prefill: partials in the workspace, (m, l) in a buffer of their own
+static int32_t ensure_prefill_split(bg_kv_cache* c, size_t floats) {
+  int32_t rc = ensure_workspace_floats(c, floats, 0);
+  if (rc != BG_OK || c->pf_ml) return rc;
+  hipError_t e = hipMalloc((void**)&c->pf_ml, bg::prefill_split_ml_bytes());
+  if (e != hipSuccess) {
+    c->pf_ml = nullptr;
+    return hip_fail(e, "split prefill (m, l) allocation");
+  }
+  return BG_OK;
+}
+
+static int32_t ensure_workspace(bg_kv_cache* c, int S, int H) {
+  size_t counters = 0;
+  size_t need = bg::decode_workspace_floats(view(c, 0), S, H, c->num_cus, &counters);
+  if (c->dtype == BG_KV_F32) {
+    const size_t f = bg::f32_workspace_floats(view(c, 0), S, H);
+    need = f > need ? f : need;
+  }
+  return ensure_workspace_floats(c, need, counters);
 }
 
 // the f16 prefill copy holds one layer at the cache's physical capacity (zero-filled, so slots
@@ -629,9 +655,13 @@ static int32_t ensure_prefill_copy(bg_kv_cache* c) {
 
 int32_t bg_attention_reserve(bg_kv_cache* c, int32_t S, int32_t H) {
   if (!c || S < 1 || H < 1 || H % c->kv_heads) return fail(BG_E_INVALID, "bg_attention_reserve: bad arguments");
-  if (bg::prefill_wants_f16_copy(view(c, 0), S, H) && !bg::decode_supported(view(c, 0), S, H)) {
-    int32_t rc = ensure_prefill_copy(c);
-    if (rc != BG_OK) return rc;
+  if (c->dtype != BG_KV_F32 && !bg::decode_preferred(view(c, 0), S, H)) {
+    if (bg::prefill_wants_f16_copy(view(c, 0), S, H)) {
+      int32_t rc = ensure_prefill_copy(c);
+      if (rc != BG_OK) return rc;
+    }
+    const size_t pf = bg::prefill_workspace_floats_max(view(c, 0), S, H, c->num_cus);
+    return pf > 0 ? ensure_prefill_split(c, pf) : BG_OK;
   }
   if (!bg::decode_supported(view(c, 0), S, H) && !bg::f32_split_supported(view(c, 0), S, H)) return BG_OK;
   return ensure_workspace(c, S, H);
@@ -671,6 +701,7 @@ static bg::AttnArgs attention_args(bg_kv_cache* c, const float* q, int32_t S, in
   a.out = out;
   a.ws_o = nullptr;
   a.ws_ml = nullptr;
+  a.pf_ml = nullptr;
   a.ws_count = nullptr;
   a.ws_floats = 0;
   a.num_cus = c->num_cus;
@@ -701,7 +732,7 @@ int32_t bg_attention(bg_kv_cache* c, int32_t layer, const float* q, int32_t S, i
     e = bg::launch_attention_f32_split(L, a, st);
   } else if (c->dtype == BG_KV_F32) {
     e = bg::launch_attention_f32(L, a, st);
-  } else if (bg::decode_supported(L, S, H)) {
+  } else if (bg::decode_preferred(L, S, H)) {
     int32_t rc = ensure_workspace(c, S, H);
     if (rc != BG_OK) return rc;
     a.ws_o = c->ws;
@@ -709,6 +740,14 @@ int32_t bg_attention(bg_kv_cache* c, int32_t layer, const float* q, int32_t S, i
     a.ws_floats = c->ws_floats;
     e = bg::launch_attention_decode(L, a, st);
   } else if (bg::prefill_supported(L, S, H)) {
+    const size_t pf = bg::prefill_workspace_floats(L, S, H, pos_base, c->num_cus);
+    if (pf > 0) {
+      int32_t rc = ensure_prefill_split(c, pf);
+      if (rc != BG_OK) return rc;
+      a.ws_o = c->ws;
+      a.ws_floats = c->ws_floats;
+      a.pf_ml = c->pf_ml;
+    }
     if (bg::prefill_wants_f16_copy(L, S, H)) {
       // dequantize the attended slots once, then run the f16 path on the copy
       int32_t rc = ensure_prefill_copy(c);
@@ -769,7 +808,7 @@ int32_t bg_attention_noalloc(bg_kv_cache* c, int32_t layer, const float* q, int3
   if (c->dtype == BG_KV_F32) {
     // the exact-f32 kernel of one wave per (query, head) keeps no partials
     e = bg::launch_attention_f32(L, a, st);
-  } else if (bg::decode_supported(L, S, H)) {
+  } else if (bg::decode_preferred(L, S, H)) {
     bg::DecodePlan pl;
     // the most splits any occupancy gives (a lower residency only merges splits)
     if (!bg::decode_plan(L, S, H, pos_base, c->num_cus, 1 << 20, &pl)) return fail(BG_E_UNSUPPORTED, "decode plan");
@@ -781,7 +820,13 @@ int32_t bg_attention_noalloc(bg_kv_cache* c, int32_t layer, const float* q, int3
     a.ws_floats = kScratchBytes / sizeof(float);
     e = bg::launch_attention_decode(L, a, st);
   } else if (bg::prefill_supported(L, S, H)) {
-    // a q8 cache is staged in-kernel (no f16 copy): the same values, so the same results
+    // a q8 cache is staged in-kernel (no f16 copy): the same values, so the same results; a
+    // split-K prefill keeps its partials in the scratch (the split plan caps them below it)
+    if (bg::prefill_split_ml_bytes() > kScratchMlBytes)
+      return fail(BG_E_UNSUPPORTED, "bg_attention_noalloc: the scratch's (m, l) area is smaller than a split prefill needs");
+    a.ws_o = (float*)ptr;
+    a.ws_floats = kScratchBytes / sizeof(float);
+    a.pf_ml = (float*)((char*)ptr + kScratchBytes);
     e = bg::launch_attention_prefill(L, a, st);
   } else {
     return fail(BG_E_UNSUPPORTED, "bg_attention_noalloc: no kernel for S %d, heads %d", S, H);

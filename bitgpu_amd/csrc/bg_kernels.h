@@ -86,6 +86,9 @@ struct AttnArgs {
   float* out;
   // split-K workspace
   float* ws_o; float* ws_ml; unsigned* ws_count; size_t ws_floats;
+  // split-K prefill: (m, l) of the partials, prefill_split_ml_bytes() long (outside ws_o, whose
+  // slots hold the empty marker between launches)
+  float* pf_ml;
   int num_cus;
   // decode merge: host-visible error word, poll bound (0: default) and a test hook that makes
   // one split store no partial (-1: none)
@@ -105,6 +108,10 @@ uint32_t decode_workspace_empty();
 // floats of the split partials one decode launch with n_splits splits per kv head writes
 size_t decode_partial_floats(const LayerView& L, int S, int H, int n_splits);
 bool decode_supported(const LayerView& L, int S, int H);
+// the dispatch: decode kernel (true) or prefill kernel for S rows of H heads. Decode takes every
+// shape whose rows per kv head fit one 16-row set, and every sink-mode shape it supports; more
+// rows go to the (split-K) prefill, except q8 at head_dim 128 up to 24 rows (measured faster).
+bool decode_preferred(const LayerView& L, int S, int H);
 // the split-K plan of a decode launch (host-only arithmetic; false when the kernel does not take
 // the shape). resident_per_cu: workgroups of the launch's instantiation a CU holds at once.
 struct DecodePlan {
@@ -117,5 +124,14 @@ bool prefill_supported(const LayerView& L, int S, int H);
 // a q8 prefill of S rows that stages each K/V tile for enough query blocks to run faster on an
 // f16 copy of the attended slots
 bool prefill_wants_f16_copy(const LayerView& L, int S, int H);
+// "not written yet" marker of a split partial slot: a quiet NaN with a payload arithmetic on
+// finite inputs never produces. The decode and split-K prefill kernels share the workspace and
+// both leave every slot they use holding it.
+constexpr uint32_t kWorkspaceEmpty = 0x7FF1DE5Au;
+// workspace floats a prefill launch's split-K partials use at pos_base (0: the launch does not
+// split); the most any pos_base can use for S rows of H heads is prefill_workspace_floats_max
+size_t prefill_workspace_floats(const LayerView& L, int S, int H, int pos_base, int num_cus);
+size_t prefill_workspace_floats_max(const LayerView& L, int S, int H, int num_cus);
+size_t prefill_split_ml_bytes();
 
 }  // namespace bg

@@ -115,7 +115,7 @@ struct DecodeParams {
 
 // "not written yet" marker of a partial slot: a quiet NaN with a payload that arithmetic on
 // finite inputs never produces
-constexpr uint32_t kPartialEmpty = 0x7FF1DE5Au;
+constexpr uint32_t kPartialEmpty = kWorkspaceEmpty;
 constexpr int kUnitF4 = 17;  // float4 per (unit, split) slot
 // splits per kv head at most (the merge holds a column of every split in registers)
 constexpr int kMaxSplits = 256;
@@ -860,6 +860,14 @@ bool decode_supported(const LayerView& L, int S, int H) {
   // more rows than the operand and P^T tiles fit in LDS (D=256: about 20) go to the prefill kernel
   const int nw_max = (L.D == 128 && nset_for(R) == 1) ? 8 : 4;
   return R >= 1 && nset_for(R) <= 3 && decode_lds_bytes(L.D, L.dtype, R, nw_max) <= kDecodeLdsMax;
+}
+
+bool decode_preferred(const LayerView& L, int S, int H) {
+  if (!decode_supported(L, S, H)) return false;
+  const int R = (H / L.kv_heads) * S;
+  if (R <= 16 || L.ring.roll) return true;  // one row set, or read-time rotation
+  if (L.D == 256) return false;             // more row sets at D=256 spill
+  return L.dtype == KV_Q8 && R <= 24;
 }
 
 // Split-K plan of one decode launch. Waves: D=128 single-set shapes run 8-wave workgroups (every

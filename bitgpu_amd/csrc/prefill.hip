@@ -36,6 +36,7 @@
 //   O^T += V^T P^T  v_mfma_f32_32x32x16_f16: the S^T accumulator registers are already in the
 //             B-operand layout of P^T for the V tile's panel order, no transpose.
 // The output gate (gate_sigmoid.wgsl:13) is applied at the store.
+#include <algorithm>
 #include <type_traits>
 
 #include "bg_kernels.h"
@@ -76,6 +77,12 @@ struct PrefillParams {
   int n_scan_fixed;  // >0: scan this many physical slots for every block (sink mode after a wrap)
   int phys_limit;
   int mirror;        // pair items heavy / light over the one wave of the grid (see the kernel)
+  // split-K: n_parts > 1 splits every item's key range into parts of part_steps steps, each
+  // scanned by its own workgroup, which leaves its partial in pws for prefill_merge_kernel
+  int n_parts, part_steps;
+  int split_waves;   // waves whose rows can be valid (fewer when the grid has fewer rows than 128)
+  float4* pws;       // [item][part][split_waves][4 * D/32][64] float4: o slots (empty marker between launches)
+  float2* pml;       // [item][part][split_waves][64] (m, l) of each lane's row
 };
 
 template <int D>
@@ -333,10 +340,14 @@ __global__ __launch_bounds__(256, D == 128 ? 2 : 1) void prefill_kernel(PrefillP
   // the CUs hold at once (mirror) pairs them: workgroup b < n/2 takes item b, the rest the mirrors
   // n-1-(b-n/2), so that each CU holds one heavy and one light item and every CU scans about the
   // same number of keys. A larger grid runs heaviest first, balanced by the dispatcher.
+  // Split-K (a grid far smaller than the GPU): workgroup b scans part b % n_parts of item
+  // b / n_parts.
   const int bid = blockIdx.x;
   const int n_items = p.n_qblocks * KV;
   const int half = (n_items + 1) / 2;
-  const int item = !p.mirror || bid < half ? bid : n_items - 1 - (bid - half);
+  const bool split = p.n_parts > 1;
+  const int part = split ? bid % p.n_parts : 0;
+  const int item = split ? bid / p.n_parts : !p.mirror || bid < half ? bid : n_items - 1 - (bid - half);
   const int kvh = item % KV;
   const int qb = p.n_qblocks - 1 - item / KV;
   const int s0 = qb * p.QB;
@@ -350,7 +361,11 @@ __global__ __launch_bounds__(256, D == 128 ? 2 : 1) void prefill_kernel(PrefillP
   // key range of the block in KT-key steps
   const int last_q = min(s0 + p.QB, p.S) - 1;
   const int n_scan = p.n_scan_fixed > 0 ? p.n_scan_fixed : p.pos_base + last_q + 1;
-  const int steps = (n_scan + KT - 1) / KT;
+  const int steps_item = (n_scan + KT - 1) / KT;
+  // this workgroup's steps [t0, steps) of the block's key range
+  const int t0 = part * p.part_steps;
+  const int steps = split ? min(t0 + p.part_steps, steps_item) : steps_item;
+  if (t0 >= steps) return;  // a part past the block's range (the whole workgroup)
   const int t_last = steps - 1;
   // the earliest key index any row of the block masks (causal diagonal or scan end)
   const int mask_from = min(min(p.pos_base + s0 + 1, n_scan), p.phys_limit);
@@ -366,12 +381,12 @@ __global__ __launch_bounds__(256, D == 128 ? 2 : 1) void prefill_kernel(PrefillP
       qraw[2 * c + 1] = *(const float4*)(qr + 16 * c + 8 * g2 + 4);
     }
   }
-  const int j00 = 0;
+  const int j00 = t0 * KT;
   StageRegs<D, DT> R0;
   if constexpr (PIPE) {
     // K and V of the first step and K of the second (K is staged one step ahead of V)
     stg.dma(p, kvh, j00, k0, v0);
-    stg.dma_k(p, kvh, min(1, t_last) * KT, k1);
+    stg.dma_k(p, kvh, min(t0 + 1, t_last) * KT, k1);
   } else if constexpr (DMA) {
     stg.dma(p, kvh, j00, k0, v0);
   } else {
@@ -501,7 +516,7 @@ __global__ __launch_bounds__(256, D == 128 ? 2 : 1) void prefill_kernel(PrefillP
       floatx16 sacc[NA];
       PH8 pb[NSUB][2];
       qk(std::false_type{}, k0, sacc, pb);
-      raise(mask_max(0, sacc));
+      raise(mask_max(t0, sacc));
     }
     __syncthreads();  // the first K buffer and the Q operand area are free
 
@@ -539,7 +554,7 @@ __global__ __launch_bounds__(256, D == 128 ? 2 : 1) void prefill_kernel(PrefillP
       __builtin_amdgcn_s_waitcnt(0xf70);  // vmcnt(0): this wave's copies landed
       __syncthreads();
     };
-    for (int s = 0; s < steps; s += 2) {
+    for (int s = t0; s < steps; s += 2) {
       pstep(s, k1, v0, k0, v1);
       if (s + 1 < steps) pstep(s + 1, k0, v1, k1, v0);
     }
@@ -676,7 +691,7 @@ __global__ __launch_bounds__(256, D == 128 ? 2 : 1) void prefill_kernel(PrefillP
     };
 
     // ---------------- main loop, two steps per turn so the buffers are fixed arrays ----------------
-    for (int s = 0; s < steps; s += 2) {
+    for (int s = t0; s < steps; s += 2) {
       step(s, k0, v0, k1, v1);
       if (s + 1 < steps) step(s + 1, k1, v1, k0, v0);
     }
@@ -685,6 +700,20 @@ __global__ __launch_bounds__(256, D == 128 ? 2 : 1) void prefill_kernel(PrefillP
   // ---------------- store ----------------
   {
     { const float2 r = pair32(lsum); lsum = r.x + r.y; }
+    if (split) {
+      // the part's partial: lane l of wave w keeps its own layout (rows and dims as in o), so
+      // each slot is one contiguous 1 KB store; the merge runs as the next kernel on the stream
+      if (wave >= p.split_waves) return;  // no valid rows (and no barrier follows)
+      const size_t pi = ((size_t)item * p.n_parts + part) * p.split_waves + wave;
+      float4* pw = p.pws + pi * 4 * ND * 64 + lane;
+#pragma unroll
+      for (int dc = 0; dc < ND; dc++)
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+          pw[(4 * dc + k) * 64] = make_float4(o[dc][4 * k], o[dc][4 * k + 1], o[dc][4 * k + 2], o[dc][4 * k + 3]);
+      p.pml[pi * 64 + lane] = make_float2(m, lsum);
+      return;
+    }
     if constexpr (D == 128) {
       // through one LDS array per wave (16 KB, the tiles are no longer read): rows written
       // swizzled, read back and stored as contiguous 512-byte rows (the register layout
@@ -764,6 +793,82 @@ __global__ __launch_bounds__(256, D == 128 ? 2 : 1) void prefill_kernel(PrefillP
   }
 }
 
+// Split-K merge: workgroup (item, wave, o slot) combines that slot of the wave's 32 rows over the
+// parts by log-sum-exp, applies the gate (gate_sigmoid.wgsl:13 form) and stores the output
+// float4s; the four 64-lane groups take every fourth part and meet through LDS. Every o slot it
+// read gets the empty marker back, so the workspace the decode kernel shares keeps its invariant
+// (the (m, l) values live outside that workspace and are only read).
+template <int D>
+__global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillParams p) {
+  constexpr int KT = PfCfg<D>::KT, ND = D / 32, NSL = 4 * ND;
+  const int KV = p.L.kv_heads;
+  const int sl = blockIdx.x % NSL;
+  const int iw = blockIdx.x / NSL;
+  const int item = iw / p.split_waves, wave = iw % p.split_waves;
+  const int lane = threadIdx.x & 63, grp = threadIdx.x >> 6;
+  const int kvh = item % KV;
+  const int qb = p.n_qblocks - 1 - item / KV;
+  const int s0 = qb * p.QB;
+  const int n = lane & 31, g2 = lane >> 5, r = wave * 32 + n;
+  const int qi = s0 + r / p.G, h = kvh * p.G + r % p.G;
+  const bool row_ok = r < p.QB * p.G && qi < p.S;
+  const int last_q = min(s0 + p.QB, p.S) - 1;
+  const int n_scan = p.n_scan_fixed > 0 ? p.n_scan_fixed : p.pos_base + last_q + 1;
+  const int steps_item = (n_scan + KT - 1) / KT;
+  const int np = (steps_item + p.part_steps - 1) / p.part_steps;  // parts that scanned keys
+  const size_t pstride = (size_t)p.split_waves;                   // per part, in (wave) units
+  const size_t pi0 = (size_t)item * p.n_parts * p.split_waves + wave;
+  __shared__ float red_m[4][64];
+  __shared__ float4 red_o[4][64];
+  __shared__ float red_l[4][64];
+  float mx = -INFINITY;
+  for (int q = grp; q < np; q += 4) mx = fmaxf(mx, p.pml[(pi0 + q * pstride) * 64 + lane].x);
+  red_m[grp][lane] = mx;
+  __syncthreads();
+  const float M = fmaxf(fmaxf(red_m[0][lane], red_m[1][lane]), fmaxf(red_m[2][lane], red_m[3][lane]));
+  const float em = __uint_as_float(kWorkspaceEmpty);
+  const float4 empty = make_float4(em, em, em, em);
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  float lt = 0.0f;
+  for (int q = grp; q < np; q += 4) {
+    const size_t pi = pi0 + q * pstride;
+    const float2 ml = p.pml[pi * 64 + lane];
+    const float w = __builtin_amdgcn_exp2f(ml.x - M);
+    float4* slot = p.pws + (pi * NSL + sl) * 64 + lane;
+    const float4 v = *slot;
+    acc.x += v.x * w;
+    acc.y += v.y * w;
+    acc.z += v.z * w;
+    acc.w += v.w * w;
+    lt += ml.y * w;
+    *slot = empty;
+  }
+  red_o[grp][lane] = acc;
+  red_l[grp][lane] = lt;
+  __syncthreads();
+  if (grp == 0 && row_ok) {
+    float4 o = red_o[0][lane];
+    float L = red_l[0][lane];
+#pragma unroll
+    for (int g = 1; g < 4; g++) {
+      const float4 b = red_o[g][lane];
+      o.x += b.x;
+      o.y += b.y;
+      o.z += b.z;
+      o.w += b.w;
+      L += red_l[g][lane];
+    }
+    const int d = 32 * (sl >> 2) + 8 * (sl & 3) + 4 * g2;
+    float rr[4] = {o.x / L, o.y / L, o.z / L, o.w / L};
+    if (p.gate) {
+      const float* gr = p.gate + ((size_t)qi * p.H + h) * p.gate_stride + d;
+#pragma unroll
+      for (int e = 0; e < 4; e++) rr[e] = rr[e] / (1.0f + expf(-gr[e]));
+    }
+    *(float4*)(p.out + ((size_t)qi * p.H + h) * D + d) = make_float4(rr[0], rr[1], rr[2], rr[3]);
+  }
+}
+
 bool prefill_supported(const LayerView& L, int S, int H) {
   if (L.dtype == KV_F32) return false;
   if (L.D != 128 && L.D != 256) return false;
@@ -787,10 +892,69 @@ bool prefill_wants_f16_copy(const LayerView& L, int S, int H) {
 // dispatcher.
 static bool pf_mirror(const LayerView& L, int n_items, int num_cus) { return L.D == 128 && n_items <= 2 * num_cus; }
 
+// Split-K plan of a prefill launch. A grid of (query block, kv head) items far smaller than the
+// GPU (short prompts after a long context, speculative verify with many heads per kv head) leaves
+// most CUs idle while each workgroup scans the whole key range; such a grid is split into parts
+// of at least kPfMinPartSteps steps, up to a full GPU's worth of workgroups, with all partials
+// within kPfSplitMaxBytes (the allocation-free entry point's scratch holds them too, so both
+// entry points make the same split and return the same results).
+constexpr size_t kPfSplitMaxBytes = (size_t)8 << 20;
+constexpr int kPfMinPartSteps = 4;
+constexpr size_t kPfSplitMlBytes = (size_t)256 << 10;  // (m, l) of the split partials
+struct PfSplitPlan {
+  int n_parts, part_steps, waves;
+  size_t floats;
+};
+static PfSplitPlan pf_split_plan(const LayerView& L, int S, int H, int pos_base, int num_cus) {
+  PfSplitPlan r{1, 0, 4, 0};
+  const int G = H / L.kv_heads, QB = 128 / G;
+  const int n_items = (S + QB - 1) / QB * L.kv_heads;
+  const int KT = L.D == 128 ? PfCfg<128>::KT : PfCfg<256>::KT;
+  const int per_cu = L.D == 128 ? 2 : 1;  // workgroups a CU holds
+  const long slots = (L.ring.roll && L.ring.head != 0) ? (long)L.max_seq : (long)pos_base + S;
+  const int steps_max = (int)((slots + KT - 1) / KT);
+  if (2 * n_items > per_cu * num_cus) return r;
+  // partials only for the waves holding rows: (query, head) rows of a block, 32 a wave
+  const int waves = std::min(4, (std::min(QB, S) * G + 31) / 32);
+  const size_t part_bytes = (size_t)waves * 4 * (L.D / 32) * 64 * sizeof(float4);
+  const size_t ml_bytes = (size_t)waves * 64 * sizeof(float2);
+  int P = per_cu * num_cus / n_items;
+  P = std::min(P, steps_max / kPfMinPartSteps);
+  P = std::min(P, (int)(kPfSplitMaxBytes / (part_bytes * n_items)));
+  P = std::min(P, (int)(kPfSplitMlBytes / (ml_bytes * n_items)));
+  if (P < 2) return r;
+  const int ps = (steps_max + P - 1) / P;
+  const int np = (steps_max + ps - 1) / ps;
+  if (np < 2) return r;
+  r.n_parts = np;
+  r.part_steps = ps;
+  r.waves = waves;
+  r.floats = (size_t)n_items * np * part_bytes / sizeof(float);
+  return r;
+}
+
+size_t prefill_workspace_floats(const LayerView& L, int S, int H, int pos_base, int num_cus) {
+  if (!prefill_supported(L, S, H)) return 0;
+  return pf_split_plan(L, S, H, pos_base, num_cus).floats;
+}
+
+size_t prefill_split_ml_bytes() { return kPfSplitMlBytes; }
+
+size_t prefill_workspace_floats_max(const LayerView& L, int S, int H, int num_cus) {
+  if (!prefill_supported(L, S, H)) return 0;
+  const int G = H / L.kv_heads, QB = 128 / G;
+  const int n_items = (S + QB - 1) / QB * L.kv_heads;
+  const int per_cu = L.D == 128 ? 2 : 1;
+  if (2 * n_items > per_cu * num_cus) return 0;
+  return kPfSplitMaxBytes / sizeof(float);
+}
+
 template <int D, int DT, bool ROLL>
 static hipError_t launch_pf(const PrefillParams& p, hipStream_t st) {
-  const int n_wg = p.n_qblocks * p.L.kv_heads;
-  hipLaunchKernelGGL((prefill_kernel<D, DT, ROLL>), dim3(n_wg), dim3(256), 0, st, p);
+  const int n_items = p.n_qblocks * p.L.kv_heads;
+  hipLaunchKernelGGL((prefill_kernel<D, DT, ROLL>), dim3(n_items * p.n_parts), dim3(256), 0, st, p);
+  if (p.n_parts > 1)
+    hipLaunchKernelGGL((prefill_merge_kernel<D>), dim3(n_items * p.split_waves * 4 * (D / 32)), dim3(256), 0, st, p);
   return hipGetLastError();
 }
 
@@ -811,6 +975,21 @@ hipError_t launch_attention_prefill(const LayerView& L, const AttnArgs& a, hipSt
   p.n_scan_fixed = (L.ring.roll && L.ring.head != 0) ? L.max_seq : 0;
   p.phys_limit = L.ring.roll ? L.max_seq : L.cap;
   p.mirror = pf_mirror(L, p.n_qblocks * L.kv_heads, a.num_cus);
+  p.n_parts = 1;
+  p.part_steps = 0;
+  p.split_waves = 4;
+  p.pws = nullptr;
+  p.pml = nullptr;
+  const PfSplitPlan sp = pf_split_plan(L, a.S, a.H, a.pos_base, a.num_cus);
+  if (sp.n_parts > 1) {
+    if (!a.ws_o || !a.pf_ml || sp.floats > a.ws_floats) return hipErrorInvalidValue;  // the caller sizes them
+    p.n_parts = sp.n_parts;
+    p.part_steps = sp.part_steps;
+    p.split_waves = sp.waves;
+    p.pws = (float4*)a.ws_o;
+    p.pml = (float2*)a.pf_ml;
+    p.mirror = 0;
+  }
   const bool roll = L.ring.roll != 0;
   if (L.D == 128) {
     if (L.dtype == KV_Q8) return roll ? launch_pf<128, KV_Q8, true>(p, st) : launch_pf<128, KV_Q8, false>(p, st);

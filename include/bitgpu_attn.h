@@ -17,8 +17,9 @@
  *     one split workspace and one f16 prefill copy, so two bg_attention calls on different
  *     streams could overlap on the GPU and corrupt each other's partials.
  *   - Kernels never allocate. Host-side allocations happen only in bg_kv_create, bg_kv_grow,
- *     bg_attention_reserve, lazily on the first bg_attention that needs more workspace or, for a
- *     q8 cache, the f16 copy a long prefill runs on, and in the snapshot transfers (a staging
+ *     bg_attention_reserve, lazily on the first bg_attention that needs more workspace (split
+ *     partials; a split-K prefill also a 256 KiB buffer of their (m, l) values) or, for a q8
+ *     cache, the f16 copy a long prefill runs on, and in the snapshot transfers (a staging
  *     buffer kept by the cache, grown when a larger region is transferred).
  *   - The decode kernel's split merge waits a bounded time for the partials of its own grid.
  *     If a wait gives up (the GPU shared with work that keeps the grid from running at once),
@@ -210,8 +211,11 @@ int32_t bg_qkv_proj_prologue(bg_kv_cache* cache, int32_t layer, const float* x, 
  * attends every resident slot <= pos_base + s. scale: the softmax scale (the dense kernels use
  * 1/sqrt(head_dim), attention_sg.wgsl:24; the hybrid passes 1/sqrt(head_dim) as a param).
  * gate (nullable): [S, H, gate_stride], out = attn / (1 + exp(-gate)) (gate_sigmoid.wgsl:13).
- * out: [S, H, head_dim] f32. Small S runs the split-K decode kernel, large S the MFMA prefill
- * kernel; f32 storage runs an exact-f32 kernel. */
+ * out: [S, H, head_dim] f32. Rows per kv head (S x H / KV) that fit one 16-row set run the
+ * split-K decode kernel (and so does sink mode up to 48 rows, and q8 at head_dim 128 up to 24);
+ * more run the MFMA prefill kernel, whose grid is split along the key range (a second kernel
+ * merging the parts) when it holds far fewer query blocks than the GPU has CUs; f32 storage runs
+ * an exact-f32 kernel. */
 int32_t bg_attention(bg_kv_cache* cache, int32_t layer, const float* q, int32_t S, int32_t H,
                      int32_t pos_base, float scale, const float* gate, int32_t gate_stride,
                      float* out, void* stream);
@@ -219,9 +223,10 @@ int32_t bg_attention(bg_kv_cache* cache, int32_t layer, const float* q, int32_t 
 /* Allocation-free variant of bg_attention. No counterpart in the reference (WebGPU dispatches
  * never allocate per call); it is for callers that cannot call hipMalloc: code under HIP graph
  * capture, tight serving loops, harnesses that forbid allocation. Same arguments and results as
- * bg_attention, but it allocates nothing: the decode kernel's split partials live in a
- * file-scope device array of 8 MiB per GPU (held until the process ends) instead of the
- * cache's workspace; a q8 prefill stages its tiles in-kernel instead of through the f16 copy
+ * bg_attention, but it allocates nothing: the split partials of the decode kernel and of a
+ * split-K prefill live in a file-scope device array of 8 MiB per GPU (plus 256 KiB for a split
+ * prefill's (m, l) values; held until the process ends) instead of the cache's workspace (the
+ * prefill splits only as far as 8 MiB of partials, for either entry point); a q8 prefill stages its tiles in-kernel instead of through the f16 copy
  * (the same values: identical output); an f32 cache runs the exact-f32 kernel of one wave per
  * (query, head), which keeps no partials (agrees with bg_attention to f32 rounding). A launch
  * whose partials would exceed the array is rejected with BG_E_INVALID before anything runs.
@@ -235,7 +240,8 @@ int32_t bg_attention_noalloc(bg_kv_cache* cache, int32_t layer, const float* q, 
 
 /* Pre-size the split-K workspace for up to S query rows of H heads (otherwise sized on first
  * use), and for a q8 cache whose prefill of S rows runs on an f16 copy of the attended slots,
- * allocate that copy. Call before capturing bg_attention into a HIP graph. */
+ * allocate that copy; for a prefill of S rows that can split along the key range, its partials
+ * and (m, l) buffer. Call before capturing bg_attention into a HIP graph. */
 int32_t bg_attention_reserve(bg_kv_cache* cache, int32_t S, int32_t H);
 
 /* ---- sink-mode eviction (overflow 'sinks') ------------------------------------------------

@@ -52,6 +52,24 @@ def fill_cache_raw(cache, li, k, v, row0=0):
     cache.append_kv(t(v), BG_V, li, L * KV, row0 * KV)
 
 
+def run_attention_noalloc(cache, li, q, pos_base, scale=None, gate=None):
+    """bg_attention_noalloc through the C ABI (torch tensors in, numpy out after a sync)."""
+    import ctypes as C
+    from bitgpu_amd import _lib
+    S, H, D = q.shape
+    qt = t(q)
+    gt = t(gate) if gate is not None else None
+    out = torch.full((S, H, D), float("nan"), dtype=torch.float32, device=DEV)
+    if scale is None:
+        scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+    st = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    _lib.check(_lib.lib().bg_attention_noalloc(cache.handle, li, C.c_void_p(qt.data_ptr()), S, H, pos_base,
+                                               float(scale), None if gt is None else C.c_void_p(gt.data_ptr()),
+                                               D if gt is not None else 0, C.c_void_p(out.data_ptr()), st))
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
 def run_attention(cache, li, q, pos_base, scale=None, gate=None):
     S, H, D = q.shape
     g = t(gate) if gate is not None else None

@@ -17,7 +17,7 @@ from bitgpu_amd import engine as E
 from bitgpu_amd import workloads as W
 from oracle import ref
 from tests.conftest import cosine, rel_err
-from tests.gpu_helpers import cached_values, fill_cache_raw, rope_dev, run_attention, t
+from tests.gpu_helpers import cached_values, fill_cache_raw, rope_dev, run_attention, run_attention_noalloc, t
 
 pytestmark = pytest.mark.gpu
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -143,7 +143,8 @@ def test_decode_gate_hybrid_shape(dev):
 # the cache's workspace (slots hold an "empty" marker between launches) and the first splits of a
 # kv head merge one (row, 64-dim) unit each. Shapes: (24,4,256) L=4097 -> 52 splits, 24 units;
 # (16,2,128) L=32768 -> 128 splits (one poll batch of 128); (2,2,128) -> 128 splits of one row;
-# (4,1,256) L=32768 -> 256 splits, polled in four batches of 64; (32,8,128) S=12 -> 48 rows.
+# (4,1,256) L=32768 -> 256 splits, polled in four batches of 64; (32,8,128) S=12 -> 48 rows per kv
+# head (past one 16-row set: the split-K prefill kernel and its merge).
 @pytest.mark.parametrize("dtype", ["f16", "q8"])
 @pytest.mark.parametrize("H,KV,D,L,S,gate", [(24, 4, 256, 4097, 1, True), (16, 2, 128, 32768, 1, False),
                                              (2, 2, 128, 32768, 1, False), (4, 1, 256, 32768, 1, False),
@@ -250,7 +251,9 @@ def test_segmented_prefill_equals_single(dev):
 def test_q8_prefill_copy_matches_staging(dev, H, KV, D, gate):
     """A q8 prefill of four or more query blocks runs on an f16 copy of the attended slots; the
     copy holds exactly the values the q8 staging produces, so it must give the bit-identical
-    output of segments short enough (three blocks) to stage from the q8 cache directly."""
+    output of the same launch staged from the q8 cache directly (the allocation-free entry point
+    stages in-kernel and makes the same split decisions). Segments of three blocks (a grid small
+    enough to split its key ranges) match the oracle."""
     G = H // KV
     QB = 128 // G
     seg, nseg = 3 * QB, 4
@@ -266,10 +269,12 @@ def test_q8_prefill_copy_matches_staging(dev, H, KV, D, gate):
     whole = run_attention(c, 0, q, 0, scale=scale, gate=g)
     parts = [run_attention(c, 0, q[i * seg:(i + 1) * seg], i * seg, scale=scale,
                            gate=None if g is None else g[i * seg:(i + 1) * seg]) for i in range(nseg)]
-    assert np.array_equal(np.concatenate(parts), whole)
+    staged = run_attention_noalloc(c, 0, q, 0, scale=scale, gate=g)
+    assert np.array_equal(staged, whole)
     kk, vv = cached_values(c, 0, 0, S)
     exp = ref.gated_attention(q, kk, vv, g, 0) if gate else ref.attention(q, kk, vv, 0, scale=scale)
     _check("q8", whole, exp)
+    _check("q8", np.concatenate(parts), exp)
     c.close()
 
 

@@ -13,7 +13,7 @@ import torch
 from bitgpu_amd import _lib
 from bitgpu_amd import engine as E
 from bitgpu_amd._lib import BitgpuError
-from tests.gpu_helpers import fill_cache_raw, t
+from tests.gpu_helpers import fill_cache_raw, rope_dev, t
 
 pytestmark = pytest.mark.gpu
 
@@ -47,6 +47,8 @@ CASES = [
     ("q8", 32, 8, 128, 2048, [(600, 2048), (130, 700)], False),      # prefill: copy path vs in-kernel
     ("f16", 32, 8, 128, 2048, [(512, 2048), (64, 300)], False),      # f16 prefill
     ("f32", 16, 8, 128, 2048, [(1, 513), (1, 100)], False),          # f32 decode (C1 shape)
+    ("q8", 24, 4, 256, 8448, [(8, 8448), (4, 3000)], True),          # split-K prefill (hybrid verify)
+    ("f16", 32, 8, 128, 8192, [(64, 8128), (32, 2000)], False),      # split-K prefill chunk
 ]
 
 
@@ -69,9 +71,12 @@ def test_noalloc_matches_bg_attention(dev, dtype, H, KV, D, L, calls, gated):
 
 
 def test_noalloc_rejects_partials_beyond_the_scratch(dev):
-    # 200 kv heads x 48 rows x 2 splits of partials = 10.4 MB > the 8 MiB scratch
+    # 200 kv heads x 48 rows x 2 splits of decode partials = 10.4 MB > the 8 MiB scratch (a
+    # sink-mode cache: its 48-row verify stays on the decode kernel)
     H = KV = 200
-    c = E.KvCache(1, KV, 128, "q8", max_seq_len=4096, capacity=4096)
+    c = E.KvCache(1, KV, 128, "q8", max_seq_len=4096, overflow="sinks", sink_tokens=4)
+    cos_d, sin_d, _, _ = rope_dev(1e6, 128, 4096)
+    c.set_rope(cos_d, sin_d)
     q = t(np.zeros((48, H, 128), np.float32))
     with pytest.raises(BitgpuError, match="beyond the 8388608-byte scratch") as ei:
         _noalloc(c, 0, q, 48, H, 4096 - 48)
