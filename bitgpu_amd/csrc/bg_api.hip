@@ -11,6 +11,7 @@
 #include <mutex>
 #include <set>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "../../include/bitgpu_attn.h"
@@ -38,6 +39,10 @@ struct bg_kv_cache {
   // f16 copy of one q8 layer's attended slots for long prefills (K then V, cap_copy slots each)
   void* pf16 = nullptr;
   float* pf_ml = nullptr;  // split-K prefill (m, l), bg::prefill_split_ml_bytes() once allocated
+  // workspaces replaced by a larger one, kept until destroy: launches captured in a graph before
+  // the growth still use them (and find their slots holding the empty marker)
+  std::vector<std::pair<float*, size_t>> retired_ws;
+  std::vector<unsigned*> retired_count;
   int pf16_cap = 0;
   int num_cus = 256;
   int q8_row = 0;     // q8: one scale per row (bg_kv_set_q8_block with head_dim)
@@ -175,6 +180,8 @@ int32_t take_merge_error(bg_kv_cache* c, hipStream_t st) {
   hipError_t e = hipDeviceSynchronize();
   if (e == hipSuccess && c->ws)
     e = hipMemsetD32((hipDeviceptr_t)c->ws, (int)bg::decode_workspace_empty(), c->ws_floats);
+  for (const auto& r : c->retired_ws)
+    if (e == hipSuccess) e = hipMemsetD32((hipDeviceptr_t)r.first, (int)bg::decode_workspace_empty(), r.second);
   int dev = 0;
   if (e == hipSuccess) e = hipGetDevice(&dev);
   if (e == hipSuccess && dev >= 0 && dev < kMaxDevices) {
@@ -427,6 +434,8 @@ int32_t bg_kv_destroy(bg_kv_cache* c) {
   if (c->ws_count) (void)hipFree(c->ws_count);
   if (c->pf16) (void)hipFree(c->pf16);
   if (c->pf_ml) (void)hipFree(c->pf_ml);
+  for (const auto& r : c->retired_ws) (void)hipFree(r.first);
+  for (unsigned* r : c->retired_count) (void)hipFree(r);
   delete c;
   return BG_OK;
 }
@@ -587,27 +596,33 @@ static int32_t ensure_workspace_floats(bg_kv_cache* c, size_t need, size_t count
   if (need < c->ws_floats) need = c->ws_floats;
   if (counters < c->ws_counters) counters = c->ws_counters;
   if (need <= c->ws_floats && counters <= c->ws_counters) return BG_OK;
-  if (c->ws) (void)hipFree(c->ws);
-  if (c->ws_count) (void)hipFree(c->ws_count);
-  c->ws = nullptr;
-  c->ws_count = nullptr;
-  c->ws_floats = 0;
-  c->ws_counters = 0;
-  hipError_t e = hipMalloc((void**)&c->ws, need * sizeof(float));
-  if (e == hipSuccess && counters) e = hipMalloc((void**)&c->ws_count, counters * sizeof(unsigned));
-  if (e == hipSuccess && counters) e = hipMemset(c->ws_count, 0, counters * sizeof(unsigned));
-  // decode split slots start out "empty"; every decode launch leaves them that way
-  if (e == hipSuccess) e = hipMemsetD32((hipDeviceptr_t)c->ws, (int)bg::decode_workspace_empty(), need);
+  // grow at least twofold, so that few workspaces are ever retired
+  if (need < 2 * c->ws_floats) need = 2 * c->ws_floats;
+  float* ws = nullptr;
+  unsigned* cnt = nullptr;
+  hipError_t e = hipMalloc((void**)&ws, need * sizeof(float));
+  if (e == hipSuccess && counters) e = hipMalloc((void**)&cnt, counters * sizeof(unsigned));
+  if (e == hipSuccess && counters) e = hipMemset(cnt, 0, counters * sizeof(unsigned));
+  // split slots start out "empty"; every launch leaves them that way
+  if (e == hipSuccess) e = hipMemsetD32((hipDeviceptr_t)ws, (int)bg::decode_workspace_empty(), need);
   if (e == hipSuccess) e = hipDeviceSynchronize();
   if (e != hipSuccess) {
-    if (c->ws) (void)hipFree(c->ws);
-    if (c->ws_count) (void)hipFree(c->ws_count);
-    c->ws = nullptr;
-    c->ws_count = nullptr;
-    return hip_fail(e, "attention workspace allocation");
+    // the old workspace stays in use
+    if (ws) (void)hipFree(ws);
+    if (cnt) (void)hipFree(cnt);
+    (void)hipGetLastError();
+    return fail(e == hipErrorOutOfMemory ? BG_E_OOM : BG_E_DEVICE, "attention workspace allocation: %s",
+                hipGetErrorString(e));
   }
+  // launches captured before keep using the old buffers: retire them instead of freeing
+  if (c->ws) c->retired_ws.emplace_back(c->ws, c->ws_floats);
+  if (c->ws_count && cnt) c->retired_count.push_back(c->ws_count);
+  c->ws = ws;
   c->ws_floats = need;
-  c->ws_counters = counters;
+  if (cnt) {
+    c->ws_count = cnt;
+    c->ws_counters = counters;
+  }
   return BG_OK;
 }
 

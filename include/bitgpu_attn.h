@@ -241,9 +241,9 @@ int32_t bg_attention_noalloc(bg_kv_cache* cache, int32_t layer, const float* q, 
 /* Pre-size the split-K workspace for up to S query rows of H heads (otherwise sized on first
  * use), and for a q8 cache whose prefill of S rows runs on an f16 copy of the attended slots,
  * allocate that copy; for a prefill of S rows that can split along the key range, its partials
- * and (m, l) buffer. Call before capturing bg_attention into a HIP graph, for every shape the
- * cache will run: a later call that needs a larger workspace reallocates it, which invalidates
- * the launches captured before (they would use the freed buffer). */
+ * and (m, l) buffer. Call before capturing bg_attention into a HIP graph (a launch under capture
+ * cannot allocate). A later call that needs a larger workspace allocates a new one and keeps the
+ * old one until bg_kv_destroy, so launches captured before stay valid. */
 int32_t bg_attention_reserve(bg_kv_cache* cache, int32_t S, int32_t H);
 
 /* ---- sink-mode eviction (overflow 'sinks') ------------------------------------------------

@@ -76,6 +76,29 @@ def test_graph_replay_matches_eager(dev, dtype, H, KV, D, L, S, gated):
     c.close()
 
 
+def test_graph_survives_workspace_growth(dev):
+    """A decode captured with only its own shape reserved; then an eager split-K prefill grows the
+    cache's workspace (a new, larger buffer): the captured decode keeps the buffer it was captured
+    with (the cache retires it instead of freeing it) and still replays to the eager result."""
+    H, KV, D, L = 24, 4, 256, 8200
+    c, q, gate = _inputs("q8", H, KV, D, L, 1, True, seed=11)
+    scale = 1.0 / 16
+    _lib.check(_lib.lib().bg_attention_reserve(c.handle, 1, H))
+    want = E.attention(c, 0, q, 1, H, L - 1, scale=scale, gate=gate, gate_stride=D)
+    out = torch.empty_like(want)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            E.attention(c, 0, q, 1, H, L - 1, scale=scale, gate=gate, gate_stride=D, out=out)
+    torch.cuda.synchronize()
+    q8 = t(np.random.default_rng(3).standard_normal((8, H, D)).astype(np.float32))
+    between = lambda: E.attention(c, 0, q8, 8, H, L - 8, scale=scale)   # split-K prefill: grows the workspace
+    _replay_and_check(graph, out, want, between)
+    c.close()
+
+
 @pytest.mark.parametrize("dtype,H,KV,D,L,S,gated", [SHAPES[0], SHAPES[2]])
 def test_graph_replay_noalloc(dev, dtype, H, KV, D, L, S, gated):
     """bg_attention_noalloc captured after an eager call: decode split partials and split-K
