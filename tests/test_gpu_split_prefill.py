@@ -87,3 +87,17 @@ def test_split_prefill_repeated_launches(dev):
         out = run_attention(c, 0, q, upto - S, scale=1.0 / 16)
         _check(out, ref.attention(q, kk[:upto], vv[:upto], upto - S, scale=1.0 / 16))
     c.close()
+
+
+@pytest.mark.parametrize("dtype,H,KV,D,L,S,gate", [
+    ("q8", 128, 1, 128, 20000, 1, False),    # one kv head, 128 rows: one item split 128 ways
+    ("f16", 64, 2, 256, 5000, 3, True),      # 96 rows per kv head at D=256, gated
+    ("q8", 64, 1, 128, 3000, 2, True),       # 128 rows, one query block of 2 queries
+])
+def test_split_prefill_extreme_shapes(dev, dtype, H, KV, D, L, S, gate):
+    c, _, q, g = _case(dtype, H, KV, D, L, S, seed=H + L, gate=gate)
+    scale = 1.0 / np.sqrt(D)
+    out = run_attention(c, 0, q, L - S, scale=scale, gate=g)
+    kk, vv = cached_values(c, 0, 0, L)
+    _check(out, ref.gated_attention(q, kk, vv, g, L - S) if gate else ref.attention(q, kk, vv, L - S, scale=scale))
+    c.close()
