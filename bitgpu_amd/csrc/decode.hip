@@ -80,11 +80,18 @@ __device__ inline float4 ldnt4(const float* p) {
 }
 
 
-// which dims lane group g feeds into QK MFMA #t (element e = 0..7 of the lane's half8)
-template <int D, bool QUARTER>
+// which dims lane group g feeds into QK MFMA #t (element e = 0..7 of the lane's half8). A pass
+// of PR = 4 query rows gives each lane group's rows a block-diagonal quarter of the MFMA's k
+// range; a pass of PR = 8 rows gives each half of the 16 rows two lane groups. With q8 codes
+// (QUARTER) the k range a row sees in one MFMA must lie in one 32-dim scale block: PR = 4 walks
+// a contiguous quarter of D per lane group; PR = 8 pairs lane groups 2h and 2h+1 on block t/2 of
+// half h (16 contiguous bytes per lane and block: MFMA t even takes bytes 0-7, odd 8-15).
+template <int D, bool QUARTER, int PR>
 __device__ inline int qk_dim(int g, int t, int e) {
-  if constexpr (QUARTER) {
+  if constexpr (QUARTER && PR == 4) {
     return g * (D / 4) + 8 * t + e;
+  } else if constexpr (QUARTER) {
+    return (g >> 1) * (D / 2) + 32 * (t >> 1) + 16 * (g & 1) + 8 * (t & 1) + e;
   } else {
     constexpr int TH = D / 64;
     return t < TH ? g * (D / 8) + 8 * t + e : D / 2 + g * (D / 8) + 8 * (t - TH) + e;
@@ -122,13 +129,13 @@ constexpr int kMaxSplits = 256;
 
 // Shared memory plan (bytes): Q operands, per-wave P^T tiles, per-wave corr; after the tile
 // loop the same space holds the per-wave partials, then the split merge's weights and sums.
-template <int D, int DT, bool ROLL, int NSET, int NW>
+template <int D, int DT, bool ROLL, int NSET, int NW, int PR>
 struct DecodeSmem {
   static constexpr bool QUARTER = (DT == KV_Q8) && !ROLL;
   static constexpr int NT = D / 32;                       // QK MFMAs per 16-slot tile
   static constexpr int NBV = (DT == KV_Q8) ? D / 32 : 1;  // P copies (one per V scale block)
   static constexpr int RS = 16 * NSET;                    // padded rows
-  static constexpr int NPMAX = RS / 4;                    // QK passes
+  static constexpr int NPMAX = RS / PR;                   // QK passes
   // + one 32-byte sink for the stores of operand slots past the last pass
   __host__ __device__ static size_t q_bytes(int np) { return (size_t)np * NT * 2 * 64 * 16 + 32; }
   static constexpr size_t p_bytes_wave = (size_t)NBV * RS * 32 * 2;
@@ -143,13 +150,16 @@ struct DecodeSmem {
 };
 
 // One wave's raw loads for a 32-slot tile (kept in flight while the previous tile computes).
-template <int D, int DT, bool QUARTER>
+template <int D, int DT, bool QUARTER, int PR>
 struct TileRegs {
   static constexpr int NB = D / 32;
   static constexpr int KU = (DT == KV_Q8) ? D / 64 : D / 32;  // uint4 of K per lane per slot
   static constexpr int VU = (DT == KV_Q8) ? NB : 2 * NB;     // uint4 of V per lane per tile
+  // K scale blocks a lane's output rows see per slot: its quarter (PR = 4) or half (PR = 8) of
+  // D with q8 codes in the MFMA; the two rope halves' blocks when rotating in f32
+  static constexpr int KSN = QUARTER ? (PR == 4 ? D / 128 : D / 64) : 2;
   uint4 kr[2][KU];
-  float ksc[2][2];
+  float ksc[2][KSN];
   uint4 vr[VU];
   float vsc[2][DT == KV_Q8 ? NB : 1];
 };
@@ -157,22 +167,26 @@ struct TileRegs {
 // The K part of a tile's loads (K codes and both scale rows: the V scales are folded into the
 // probabilities) and the V part are issued separately, so each can be re-issued for a later tile
 // as soon as its phase of the current tile has consumed it.
-template <int D, int DT, bool QUARTER>
-__device__ __forceinline__ void load_tile_k(TileRegs<D, DT, QUARTER>& T, int j0, int g, int n,
+template <int D, int DT, bool QUARTER, int PR>
+__device__ __forceinline__ void load_tile_k(TileRegs<D, DT, QUARTER, PR>& T, int j0, int g, int n,
                                             const unsigned char* kbase, const float* ksb, const float* vsb) {
   constexpr int NB = D / 32;
-  constexpr int KU = TileRegs<D, DT, QUARTER>::KU;
-  constexpr int NSUB = QUARTER ? (D / 128) : 1;
+  constexpr int KU = TileRegs<D, DT, QUARTER, PR>::KU;
+  constexpr int KSN = TileRegs<D, DT, QUARTER, PR>::KSN;
   constexpr size_t eb = (DT == KV_Q8) ? 1 : 2;
 #pragma unroll
   for (int t2 = 0; t2 < 2; t2++) {
     const int P = j0 + 16 * t2 + n;
     const unsigned char* row = kbase + (size_t)P * D * eb;
     if constexpr (QUARTER) {
+      // uint4 i holds the codes of MFMAs 2i and 2i+1 (qk_dim)
+      const int kb0 = PR == 4 ? g * (D / 4) : (g >> 1) * (D / 2) + 16 * (g & 1);
+      const int kstep = PR == 4 ? 16 : 32;
 #pragma unroll
-      for (int i = 0; i < KU; i++) T.kr[t2][i] = ld16(row + g * (D / 4) + 16 * i);
+      for (int i = 0; i < KU; i++) T.kr[t2][i] = ld16(row + kb0 + kstep * i);
+      const int sb0 = PR == 4 ? g * KSN : (g >> 1) * KSN;
 #pragma unroll
-      for (int i = 0; i < NSUB; i++) T.ksc[t2][i] = ldnt(ksb + (size_t)P * NB + g * NSUB + i);
+      for (int i = 0; i < KSN; i++) T.ksc[t2][i] = ldnt(ksb + (size_t)P * NB + sb0 + i);
     } else {
       constexpr int HU = KU / 2;  // uint4 per half piece
 #pragma unroll
@@ -198,8 +212,8 @@ __device__ __forceinline__ void load_tile_k(TileRegs<D, DT, QUARTER>& T, int j0,
   }
 }
 
-template <int D, int DT, bool QUARTER>
-__device__ __forceinline__ void load_tile_v(TileRegs<D, DT, QUARTER>& T, int j0, int g, int n,
+template <int D, int DT, bool QUARTER, int PR>
+__device__ __forceinline__ void load_tile_v(TileRegs<D, DT, QUARTER, PR>& T, int j0, int g, int n,
                                             const unsigned char* vbase) {
   constexpr int NB = D / 32;
   constexpr size_t eb = (DT == KV_Q8) ? 1 : 2;
@@ -215,27 +229,30 @@ __device__ __forceinline__ void load_tile_v(TileRegs<D, DT, QUARTER>& T, int j0,
   }
 }
 
-template <int D, int DT, bool QUARTER>
-__device__ __forceinline__ void load_tile(TileRegs<D, DT, QUARTER>& T, int j0, int g, int n,
+template <int D, int DT, bool QUARTER, int PR>
+__device__ __forceinline__ void load_tile(TileRegs<D, DT, QUARTER, PR>& T, int j0, int g, int n,
                                           const unsigned char* kbase, const unsigned char* vbase,
                                           const float* ksb, const float* vsb) {
-  load_tile_k<D, DT, QUARTER>(T, j0, g, n, kbase, ksb, vsb);
-  load_tile_v<D, DT, QUARTER>(T, j0, g, n, vbase);
+  load_tile_k<D, DT, QUARTER, PR>(T, j0, g, n, kbase, ksb, vsb);
+  load_tile_v<D, DT, QUARTER, PR>(T, j0, g, n, vbase);
 }
 
-// NPT > 0: the launch has exactly NPT passes of 4 query rows (compiled straight-line); 0: up to
-// the set's RS / 4 passes, counted at run time
-template <int D, int DT, bool ROLL, int NSET, int NW, int NPT>
+// PR: query rows per QK pass (4, or 8 for more than 4 rows: half the MFMAs, operand reads and
+// reductions per row). NPT > 0: the launch has exactly NPT passes (compiled straight-line); 0:
+// up to the set's RS / PR passes, counted at run time
+template <int D, int DT, bool ROLL, int NSET, int NW, int NPT, int PR>
 __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
-  using SM = DecodeSmem<D, DT, ROLL, NSET, NW>;
+  using SM = DecodeSmem<D, DT, ROLL, NSET, NW, PR>;
+  using TR = TileRegs<D, DT, SM::QUARTER, PR>;
   constexpr int NPK = NPT > 0 ? NPT : SM::NPMAX;  // passes compiled
   constexpr bool QUARTER = SM::QUARTER;
   constexpr int NT = SM::NT;
   constexpr int NBV = SM::NBV;
   constexpr int RS = SM::RS;
   constexpr int NB = D / 32;         // q8 scale blocks per row
-  constexpr int NSUB = QUARTER ? (D / 128) : 1;  // scale blocks inside one lane group's quarter
-  constexpr int KU = TileRegs<D, DT, QUARTER>::KU;
+  constexpr int NSUB = QUARTER ? TR::KSN : 1;  // scale blocks a lane's output rows see
+  constexpr int KU = TR::KU;
+  constexpr int RL = PR / 4;         // query rows per lane and pass after the reduction
   constexpr int NTHR = 64 * NW;
 
   extern __shared__ __align__(16) unsigned char smem[];
@@ -249,7 +266,9 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
   const int n = lane & 15;
   const int kvh = blockIdx.x % p.L.kv_heads;
   const int split = blockIdx.x / p.L.kv_heads;
-  const int NP = NPT > 0 ? NPT : (p.R + 3) >> 2;
+  const int NP = NPT > 0 ? NPT : (p.R + PR - 1) / PR;
+  // query row of pass `pass` that lane group g holds in slot i (i < RL) after the reduction
+  auto row_of = [&](int pass, int i) { return PR == 4 ? 4 * pass + g : 8 * pass + 2 * i + (g >> 1) + 4 * (g & 1); };
 
   uint4* qs = (uint4*)smem;                                           // [NP][NT][2][64]
   unsigned char* pbase = smem + SM::q_bytes(NP);
@@ -270,7 +289,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
   // Q operands (block diagonal, hi/lo f16). The setup is straight-line code -- every load is
   // unconditional (spare slots read query 0, a wave without tiles re-reads the split's last
   // tile) and spare slots store to a sink.
-  TileRegs<D, DT, QUARTER> A, B;
+  TR A, B;
   const int tile0 = t_begin + wave;
   {
     constexpr int QMAX = (NPK * NT * 64 + NTHR - 1) / NTHR;  // operand slots per thread
@@ -282,10 +301,12 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
       const int idx = i * NTHR + tid;
       const int l = idx & 63, t = (idx >> 6) % NT, pass = (idx >> 6) / NT;
       const int gg = l >> 4, ii = l & 15;
-      const int rho = 4 * pass + (ii & 3);
-      use[i] = idx < NQ && (ii >> 2) == gg && rho < p.R;
+      // A row ii: query row rho of the pass, nonzero on the k chunks of its row group's lane groups
+      const int rho = PR * pass + (ii & (PR - 1));
+      const bool diag = PR == 4 ? (ii >> 2) == gg : (ii >> 3) == (gg >> 1);
+      use[i] = idx < NQ && diag && rho < p.R;
       const int s = use[i] ? rho / p.G : 0, h = use[i] ? kvh * p.G + rho % p.G : 0;
-      const float* qr = p.q + ((size_t)s * p.H + h) * D + (use[i] ? qk_dim<D, QUARTER>(gg, t, 0) : 0);
+      const float* qr = p.q + ((size_t)s * p.H + h) * D + (use[i] ? qk_dim<D, QUARTER, PR>(gg, t, 0) : 0);
       const float4 a = *(const float4*)qr, b = *(const float4*)(qr + 4);
       qv[i][0] = a.x; qv[i][1] = a.y; qv[i][2] = a.z; qv[i][3] = a.w;
       qv[i][4] = b.x; qv[i][5] = b.y; qv[i][6] = b.z; qv[i][7] = b.w;
@@ -297,7 +318,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     __builtin_amdgcn_s_waitcnt(0xf70);  // vmcnt(0): q has arrived
     __builtin_amdgcn_sched_barrier(0);
     const int ta = tile0 < t_end ? tile0 : t_end - 1;
-    load_tile<D, DT, QUARTER>(A, ta * 32, g, n, kbase, vbase, ksb, vsb);
+    load_tile<D, DT, QUARTER, PR>(A, ta * 32, g, n, kbase, vbase, ksb, vsb);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < QMAX; i++) {
@@ -325,9 +346,11 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
   }
   __syncthreads();
 
-  float m[NPK], lsum[NPK];
+  float m[NPK][RL], lsum[NPK][RL];
 #pragma unroll
-  for (int i = 0; i < NPK; i++) { m[i] = -1e30f; lsum[i] = 0.0f; }
+  for (int i = 0; i < NPK; i++)
+#pragma unroll
+    for (int j = 0; j < RL; j++) { m[i][j] = -1e30f; lsum[i][j] = 0.0f; }
   floatx4 o[NSET][D / 16];
 #pragma unroll
   for (int s = 0; s < NSET; s++)
@@ -335,7 +358,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     for (int i = 0; i < D / 16; i++) o[s][i] = floatx4{0, 0, 0, 0};
 
   bool rescale = false;  // the last qk_softmax raised a reference max: pv rescales O first
-  auto qk_softmax = [&](const TileRegs<D, DT, QUARTER>& T, int tile) {
+  auto qk_softmax = [&](const TR& T, int tile) {
     const int j0 = tile * 32;
     // ---------------- K operands ----------------
     // K operand for QK MFMA t of 16-slot group t2: converted just in time (plain cache) or
@@ -402,14 +425,14 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
       }
     }
 
-    // ---------------- QK + online softmax, one pass per 4 query rows ----------------
+    // ---------------- QK + online softmax, one pass per PR query rows ----------------
     // The reference max of a row is raised only when a tile's max exceeds it by more than 8 (in
     // log2 units, so P <= 2^8 stays well inside f16); most tiles then leave O and l unscaled.
-    float xs[NPK][2], mts[NPK];
+    float xs[NPK][RL][2], mts[NPK][RL];
 #pragma unroll
     for (int pass = 0; pass < NPK; pass++) {
       if (pass >= NP) break;
-      float sc[2];
+      float sc[2][RL];
 #pragma unroll
       for (int t2 = 0; t2 < 2; t2++) {
         floatx4 c[NSUB];
@@ -420,7 +443,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
           H8 ahi, alo;
           ahi.u = qs[((pass * NT + t) * 2 + 0) * 64 + lane];
           alo.u = qs[((pass * NT + t) * 2 + 1) * 64 + lane];
-          const int sub = QUARTER ? (t >> 2) : 0;
+          const int sub = QUARTER ? (PR == 4 ? t >> 2 : t >> 1) : 0;
           const half8 kt = kop(t2, t);
           c[sub] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi.h, kt, c[sub], 0, 0, 0);
           c[sub] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo.h, kt, c[sub], 0, 0, 0);
@@ -437,63 +460,82 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
             v[e] = c[0][e];
           }
         }
-        // reduce-scatter over the 4 lane groups: lane group g ends with query row g of the pass.
-        // permlane32_swap(a, b) leaves lanes l < 32 with {a[l], a[l+32]} and lanes l >= 32 with
-        // {b[l-32], b[l]}; permlane16_swap does the same for odd/even row pairs.
-        const auto u0 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[0]), __float_as_uint(v[2]), false, false);
-        const auto u1 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[1]), __float_as_uint(v[3]), false, false);
-        const float k0 = __uint_as_float(u0[0]) + __uint_as_float(u0[1]);  // rows 0,1: dims of v[0]; rows 2,3: v[2]
-        const float k1 = __uint_as_float(u1[0]) + __uint_as_float(u1[1]);
-        const auto u2 = __builtin_amdgcn_permlane16_swap(__float_as_uint(k0), __float_as_uint(k1), false, false);
-        sc[t2] = __uint_as_float(u2[0]) + __uint_as_float(u2[1]);
+        // Lane group g' holds output rows 4g'..4g'+3 (v[0..3]) of the slot. permlane32_swap(a, b)
+        // leaves lanes l < 32 with {a[l], a[l+32]} and lanes l >= 32 with {b[l-32], b[l]};
+        // permlane16_swap does the same between lane groups 0/1 and 2/3.
+        if constexpr (PR == 4) {
+          // output row 4g'+e = query row e of the pass over quarter g': reduce-scatter over the
+          // 4 lane groups, lane group g ends with query row g
+          const auto u0 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[0]), __float_as_uint(v[2]), false, false);
+          const auto u1 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[1]), __float_as_uint(v[3]), false, false);
+          const float k0 = __uint_as_float(u0[0]) + __uint_as_float(u0[1]);  // rows 0,1: dims of v[0]; rows 2,3: v[2]
+          const float k1 = __uint_as_float(u1[0]) + __uint_as_float(u1[1]);
+          const auto u2 = __builtin_amdgcn_permlane16_swap(__float_as_uint(k0), __float_as_uint(k1), false, false);
+          sc[t2][0] = __uint_as_float(u2[0]) + __uint_as_float(u2[1]);
+        } else {
+          // output row 4g'+e = query row 4(g' & 1) + e of the pass over half g' >> 1: one swap
+          // adds the halves (lane groups g' and g'+2), lane group g ends with rows row_of(pass, 0)
+          // (from v[0] / v[1]) and row_of(pass, 1) (from v[2] / v[3])
+          const auto u0 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[0]), __float_as_uint(v[1]), false, false);
+          const auto u1 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[2]), __float_as_uint(v[3]), false, false);
+          sc[t2][0] = __uint_as_float(u0[0]) + __uint_as_float(u0[1]);
+          sc[t2][RL - 1] = __uint_as_float(u1[0]) + __uint_as_float(u1[1]);
+        }
       }
-      // mask + online softmax for row rho = 4*pass + g
-      const int rho = 4 * pass + g;
-      const int qi = rho / p.G;
-      const bool row_ok = rho < p.R;
-      const int limit = p.pos_base + qi;
-      float x[2];
+      // mask + online softmax for the lane's rows
 #pragma unroll
-      for (int t2 = 0; t2 < 2; t2++) {
-        const int P = j0 + 16 * t2 + n;
-        const int Lg = ROLL ? ring.logical(P) : P;  // a plain cache is never a ring
-        const bool ok = row_ok && P < p.n_scan && P < p.phys_limit && Lg <= limit;
-        x[t2] = ok ? sc[t2] : -INFINITY;
+      for (int i = 0; i < RL; i++) {
+        const int rho = row_of(pass, i);
+        const int qi = rho / p.G;
+        const bool row_ok = rho < p.R;
+        const int limit = p.pos_base + qi;
+        float x[2];
+#pragma unroll
+        for (int t2 = 0; t2 < 2; t2++) {
+          const int P = j0 + 16 * t2 + n;
+          const int Lg = ROLL ? ring.logical(P) : P;  // a plain cache is never a ring
+          const bool ok = row_ok && P < p.n_scan && P < p.phys_limit && Lg <= limit;
+          x[t2] = ok ? sc[t2][i] : -INFINITY;
+        }
+        xs[pass][i][0] = x[0];
+        xs[pass][i][1] = x[1];
+        mts[pass][i] = group16_max(fmaxf(x[0], x[1]));
       }
-      xs[pass][0] = x[0];
-      xs[pass][1] = x[1];
-      mts[pass] = group16_max(fmaxf(x[0], x[1]));
     }
     bool grow = false;
 #pragma unroll
     for (int pass = 0; pass < NPK; pass++) {
       if (pass >= NP) break;
-      grow = grow || mts[pass] > m[pass] + 8.0f;
+#pragma unroll
+      for (int i = 0; i < RL; i++) grow = grow || mts[pass][i] > m[pass][i] + 8.0f;
     }
     rescale = __any(grow);
 #pragma unroll
     for (int pass = 0; pass < NPK; pass++) {
       if (pass >= NP) break;
-      const int rho = 4 * pass + g;
-      if (rescale) {
-        const float mn = fmaxf(m[pass], mts[pass]);
-        const float corr = exp2f(m[pass] - mn);
-        lsum[pass] *= corr;
-        m[pass] = mn;
-        if (n == 0 && rho < RS) cl[rho] = corr;
-      }
-      const float p0 = exp2f(xs[pass][0] - m[pass]), p1 = exp2f(xs[pass][1] - m[pass]);
-      lsum[pass] += p0 + p1;
-      if (rho < RS) {
 #pragma unroll
-        for (int t2 = 0; t2 < 2; t2++) {
-          const int j = 16 * t2 + n;
-          const float pv = t2 ? p1 : p0;
-          const int col = tile_panel(j) * 8 + tile_index(j);
+      for (int i = 0; i < RL; i++) {
+        const int rho = row_of(pass, i);
+        if (rescale) {
+          const float mn = fmaxf(m[pass][i], mts[pass][i]);
+          const float corr = exp2f(m[pass][i] - mn);
+          lsum[pass][i] *= corr;
+          m[pass][i] = mn;
+          if (n == 0 && rho < RS) cl[rho] = corr;
+        }
+        const float p0 = exp2f(xs[pass][i][0] - m[pass][i]), p1 = exp2f(xs[pass][i][1] - m[pass][i]);
+        lsum[pass][i] += p0 + p1;
+        if (rho < RS) {
 #pragma unroll
-          for (int b = 0; b < NBV; b++) {
-            const float w = (DT == KV_Q8) ? pv * (T.vsc[t2][b] * (1.0f / 127.0f)) : pv;
-            pl[((size_t)b * RS + rho) * 32 + col] = (_Float16)w;
+          for (int t2 = 0; t2 < 2; t2++) {
+            const int j = 16 * t2 + n;
+            const float pv = t2 ? p1 : p0;
+            const int col = tile_panel(j) * 8 + tile_index(j);
+#pragma unroll
+            for (int b = 0; b < NBV; b++) {
+              const float w = (DT == KV_Q8) ? pv * (T.vsc[t2][b] * (1.0f / 127.0f)) : pv;
+              pl[((size_t)b * RS + rho) * 32 + col] = (_Float16)w;
+            }
           }
         }
       }
@@ -504,7 +546,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
   };
 
   // ---------------- PV ----------------
-  auto pv = [&](const TileRegs<D, DT, QUARTER>& T) {
+  auto pv = [&](const TR& T) {
     auto vop = [&](int b, int par) -> half8 {
       if constexpr (DT == KV_Q8) {
         return par ? q8_to_half8(T.vr[b].z, T.vr[b].w) : q8_to_half8(T.vr[b].x, T.vr[b].y);
@@ -545,18 +587,18 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
   if constexpr (DT == KV_Q8) {
     {
       const int tb = nmy > 1 ? tile0 + NW : (tile0 < t_end ? tile0 : t_end - 1);
-      load_tile<D, DT, QUARTER>(B, tb * 32, g, n, kbase, vbase, ksb, vsb);
+      load_tile<D, DT, QUARTER, PR>(B, tb * 32, g, n, kbase, vbase, ksb, vsb);
     }
     for (; it + 4 <= nmy; it += 2) {
       const int ta = tile0 + it * NW;
       qk_softmax(A, ta);
-      load_tile_k<D, DT, QUARTER>(A, (ta + 2 * NW) * 32, g, n, kbase, ksb, vsb);
+      load_tile_k<D, DT, QUARTER, PR>(A, (ta + 2 * NW) * 32, g, n, kbase, ksb, vsb);
       pv(A);
-      load_tile_v<D, DT, QUARTER>(A, (ta + 2 * NW) * 32, g, n, vbase);
+      load_tile_v<D, DT, QUARTER, PR>(A, (ta + 2 * NW) * 32, g, n, vbase);
       qk_softmax(B, ta + NW);
-      load_tile_k<D, DT, QUARTER>(B, (ta + 3 * NW) * 32, g, n, kbase, ksb, vsb);
+      load_tile_k<D, DT, QUARTER, PR>(B, (ta + 3 * NW) * 32, g, n, kbase, ksb, vsb);
       pv(B);
-      load_tile_v<D, DT, QUARTER>(B, (ta + 3 * NW) * 32, g, n, vbase);
+      load_tile_v<D, DT, QUARTER, PR>(B, (ta + 3 * NW) * 32, g, n, vbase);
     }
     // the last one to three tiles: A and B hold tiles it and it + 1
     const int r = nmy - it;
@@ -565,7 +607,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
       qk_softmax(A, ta);
       pv(A);
     }
-    if (r == 3) load_tile<D, DT, QUARTER>(A, (ta + 2 * NW) * 32, g, n, kbase, vbase, ksb, vsb);
+    if (r == 3) load_tile<D, DT, QUARTER, PR>(A, (ta + 2 * NW) * 32, g, n, kbase, vbase, ksb, vsb);
     if (r >= 2) {
       qk_softmax(B, ta + NW);
       pv(B);
@@ -580,11 +622,11 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     // end the prefetch re-reads the tile just loaded, still cached)
     for (; it + 2 <= nmy; it += 2) {
       const int ta = tile0 + it * NW;
-      load_tile<D, DT, QUARTER>(B, (ta + NW) * 32, g, n, kbase, vbase, ksb, vsb);
+      load_tile<D, DT, QUARTER, PR>(B, (ta + NW) * 32, g, n, kbase, vbase, ksb, vsb);
       qk_softmax(A, ta);
       pv(A);
       const int tn = it + 2 < nmy ? ta + 2 * NW : ta + NW;
-      load_tile<D, DT, QUARTER>(A, tn * 32, g, n, kbase, vbase, ksb, vsb);
+      load_tile<D, DT, QUARTER, PR>(A, tn * 32, g, n, kbase, vbase, ksb, vsb);
       qk_softmax(B, ta + NW);
       pv(B);
     }
@@ -603,8 +645,11 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
 #pragma unroll
   for (int pass = 0; pass < NPK; pass++) {
     if (pass >= NP) break;
-    const int rho = 4 * pass + g;
-    if (n == 0 && rho < p.R) s_mw[wave][rho] = m[pass];
+#pragma unroll
+    for (int i = 0; i < RL; i++) {
+      const int rho = row_of(pass, i);
+      if (n == 0 && rho < p.R) s_mw[wave][rho] = m[pass][i];
+    }
   }
   __syncthreads();
   constexpr int DP = SM::DP;
@@ -619,9 +664,12 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
 #pragma unroll
   for (int pass = 0; pass < NPK; pass++) {
     if (pass >= NP) break;
-    const float lt = group16_sum(lsum[pass]);
-    const int rho = 4 * pass + g;
-    if (n == 0 && rho < p.R) lw[wave * p.R + rho] = lt * __builtin_amdgcn_exp2f(m[pass] - row_max(rho));
+#pragma unroll
+    for (int i = 0; i < RL; i++) {
+      const float lt = group16_sum(lsum[pass][i]);
+      const int rho = row_of(pass, i);
+      if (n == 0 && rho < p.R) lw[wave * p.R + rho] = lt * __builtin_amdgcn_exp2f(m[pass][i] - row_max(rho));
+    }
   }
 #pragma unroll
   for (int st = 0; st < NSET; st++) {
@@ -839,14 +887,17 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
 }
 
 static int nset_for(int R) { return (R + 15) / 16; }
+// query rows per QK pass: 8 once there are more than 4
+static int rows_per_pass(int R) { return R > 4 ? 8 : 4; }
 
 // dynamic LDS of the tile loop and wave combine (DecodeSmem::total for the launch's template
 // arguments); the split merge needs less (weights and 16 float4 per split group)
-// NW: waves per workgroup (the most a shape launches with, 8 for D=128 single-set, bounds the rest)
-static size_t decode_lds_bytes(int D, int dtype, int R, int NW) {
+// NW: waves per workgroup (the most a shape launches with, 8 for D=128 single-set, bounds the rest);
+// PR: query rows per pass
+static size_t decode_lds_bytes(int D, int dtype, int R, int NW, int PR) {
   const int nset = nset_for(R);
   const int RS = 16 * nset, NT = D / 32, NBV = dtype == KV_Q8 ? D / 32 : 1;
-  const size_t a = (size_t)((R + 3) / 4) * NT * 2 * 64 * 16 + 32 + (size_t)NW * ((size_t)NBV * RS * 32 * 2 + (size_t)RS * 4);
+  const size_t a = (size_t)((R + PR - 1) / PR) * NT * 2 * 64 * 16 + 32 + (size_t)NW * ((size_t)NBV * RS * 32 * 2 + (size_t)RS * 4);
   const size_t b = (size_t)NW * R * (D + 5) * 4;
   return a > b ? a : b;
 }
@@ -857,9 +908,10 @@ bool decode_supported(const LayerView& L, int S, int H) {
   if (L.D != 128 && L.D != 256) return false;
   const int G = H / L.kv_heads;
   const int R = G * S;
-  // more rows than the operand and P^T tiles fit in LDS (D=256: about 20) go to the prefill kernel
+  // more rows than the operand and P^T tiles fit in LDS (D=256: about 20, counted with passes of
+  // 4 rows) go to the prefill kernel
   const int nw_max = (L.D == 128 && nset_for(R) == 1) ? 8 : 4;
-  return R >= 1 && nset_for(R) <= 3 && decode_lds_bytes(L.D, L.dtype, R, nw_max) <= kDecodeLdsMax;
+  return R >= 1 && nset_for(R) <= 3 && decode_lds_bytes(L.D, L.dtype, R, nw_max, 4) <= kDecodeLdsMax;
 }
 
 bool decode_preferred(const LayerView& L, int S, int H) {
@@ -882,7 +934,7 @@ bool decode_plan(const LayerView& L, int S, int H, int pos_base, int num_cus, in
   DecodePlan s;
   const int R = (H / L.kv_heads) * S;
   s.nset = nset_for(R);
-  s.passes = (R + 3) / 4;
+  s.passes = (R + rows_per_pass(R) - 1) / rows_per_pass(R);
   s.n_scan = (L.ring.roll && L.ring.head != 0) ? L.max_seq : pos_base + S;
   s.phys_limit = L.ring.roll ? L.max_seq : L.cap;
   s.n_tiles = (s.n_scan + 31) / 32;
@@ -947,14 +999,15 @@ size_t decode_workspace_floats(const LayerView& L, int S, int H, int num_cus, si
   return (size_t)L.kv_heads * R * (L.D / 64) * ns_max * kUnitF4 * 4;
 }
 
-template <int D, int DT, bool ROLL, int NSET, int NPT, int NW>
+template <int D, int DT, bool ROLL, int NSET, int NPT, int NW, int PR>
 static hipError_t launch_cfg(const LayerView& L, const AttnArgs& a, hipStream_t st) {
-  using SM = DecodeSmem<D, DT, ROLL, NSET, NW>;
-  const void* fn = (const void*)decode_kernel<D, DT, ROLL, NSET, NW, NPT>;
+  using SM = DecodeSmem<D, DT, ROLL, NSET, NW, PR>;
+  const void* fn = (const void*)decode_kernel<D, DT, ROLL, NSET, NW, NPT, PR>;
   const int R = (a.H / L.kv_heads) * a.S;
-  const int NP = (R + 3) / 4;
+  if (rows_per_pass(R) != PR) return hipErrorInvalidValue;
+  const int NP = (R + PR - 1) / PR;
   size_t smem = SM::total(NP, R);
-  if (smem != decode_lds_bytes(D, DT, R, NW)) return hipErrorInvalidValue;  // the two plans agree
+  if (smem != decode_lds_bytes(D, DT, R, NW, PR)) return hipErrorInvalidValue;  // the two plans agree
   // the merge reuses the space: weights [NS] (16-byte aligned) and [waves][16] float4
   const size_t merge_max = (((size_t)kMaxSplits * 4 + 15) & ~(size_t)15) + (size_t)NW * 16 * 16;
   smem = smem > merge_max ? smem : merge_max;
@@ -996,7 +1049,7 @@ static hipError_t launch_cfg(const LayerView& L, const AttnArgs& a, hipStream_t 
   p.err = a.err;
   p.spin_limit = a.spin_limit > 0 ? a.spin_limit : (1 << 20);
   p.withhold_split = a.withhold_split;
-  hipLaunchKernelGGL((decode_kernel<D, DT, ROLL, NSET, NW, NPT>), dim3(sp.grid), dim3(64 * NW), smem, st, p);
+  hipLaunchKernelGGL((decode_kernel<D, DT, ROLL, NSET, NW, NPT, PR>), dim3(sp.grid), dim3(64 * NW), smem, st, p);
   return hipGetLastError();
 }
 
@@ -1004,26 +1057,28 @@ template <int D, int DT, bool ROLL>
 static hipError_t launch_nset(const LayerView& L, const AttnArgs& a, int nset, hipStream_t st) {
   DecodePlan pl;
   if (!decode_plan(L, a.S, a.H, a.pos_base, a.num_cus, 1, &pl)) return hipErrorInvalidValue;
-  const int np = pl.passes;  // passes of 4 query rows
+  const int np = pl.passes;
+  const int R = (a.H / L.kv_heads) * a.S;
   switch (nset) {
     case 1: {
-      // decode shapes (G = 4 or 6 rows) get straight-line passes
+      // straight-line passes: one pass of 4 rows (G = 4 decode), one of 8 (5-8 rows: G = 6
+      // decode, short verifies), two of 8 (9-16 rows)
       if constexpr (D == 128) {
         if (pl.waves == 8) {
-          if (np == 1) return launch_cfg<D, DT, ROLL, 1, 1, 8>(L, a, st);
-          if (np == 2) return launch_cfg<D, DT, ROLL, 1, 2, 8>(L, a, st);
-          return launch_cfg<D, DT, ROLL, 1, 0, 8>(L, a, st);
+          if (R <= 4) return launch_cfg<D, DT, ROLL, 1, 1, 8, 4>(L, a, st);
+          if (np == 1) return launch_cfg<D, DT, ROLL, 1, 1, 8, 8>(L, a, st);
+          return launch_cfg<D, DT, ROLL, 1, 2, 8, 8>(L, a, st);
         }
       }
-      if (np == 1) return launch_cfg<D, DT, ROLL, 1, 1, 4>(L, a, st);
-      if (np == 2) return launch_cfg<D, DT, ROLL, 1, 2, 4>(L, a, st);
-      return launch_cfg<D, DT, ROLL, 1, 0, 4>(L, a, st);
+      if (R <= 4) return launch_cfg<D, DT, ROLL, 1, 1, 4, 4>(L, a, st);
+      if (np == 1) return launch_cfg<D, DT, ROLL, 1, 1, 4, 8>(L, a, st);
+      return launch_cfg<D, DT, ROLL, 1, 2, 4, 8>(L, a, st);
     }
     case 2:
-      // the 5-row verify of G = 4 heads (20 rows) gets its exact pass count
-      if (np == 5) return launch_cfg<D, DT, ROLL, 2, 5, 4>(L, a, st);
-      return launch_cfg<D, DT, ROLL, 2, 0, 4>(L, a, st);
-    default: return launch_cfg<D, DT, ROLL, 3, 0, 4>(L, a, st);
+      // 17-24 rows (the 5-row verify of G = 4 heads: 20) take three passes of 8
+      if (np == 3) return launch_cfg<D, DT, ROLL, 2, 3, 4, 8>(L, a, st);
+      return launch_cfg<D, DT, ROLL, 2, 0, 4, 8>(L, a, st);
+    default: return launch_cfg<D, DT, ROLL, 3, 0, 4, 8>(L, a, st);
   }
 }
 
