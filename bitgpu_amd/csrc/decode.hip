@@ -28,6 +28,7 @@
 //           BG_E_DEVICE and resets the workspace).
 // Sink mode reads unroped K and rotates it at read by the slot's logical (or absolute) position
 // (attention_sg_roll.wgsl:40-51), in f32 before the f16 conversion.
+#include <algorithm>
 #include <map>
 #include <mutex>
 #include <utility>
@@ -239,8 +240,9 @@ __device__ __forceinline__ void load_tile(TileRegs<D, DT, QUARTER, PR>& T, int j
 
 // PR: query rows per QK pass (4, or 8 for more than 4 rows: half the MFMAs, operand reads and
 // reductions per row). NPT > 0: the launch has exactly NPT passes (compiled straight-line); 0:
-// up to the set's RS / PR passes, counted at run time
-template <int D, int DT, bool ROLL, int NSET, int NW, int NPT, int PR>
+// up to the set's RS / PR passes, counted at run time. ONE: every wave has at most one tile (the
+// plan gives a split one tile a wave): no second tile in registers, so two workgroups fit a CU.
+template <int D, int DT, bool ROLL, int NSET, int NW, int NPT, int PR, bool ONE>
 __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
   using SM = DecodeSmem<D, DT, ROLL, NSET, NW, PR>;
   using TR = TileRegs<D, DT, SM::QUARTER, PR>;
@@ -584,7 +586,13 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
   // and the compiler counts them instead of draining them.
   const int nmy = tile0 < t_end ? (t_end - tile0 + NW - 1) / NW : 0;  // this wave's tiles
   int it = 0;
-  if constexpr (DT == KV_Q8) {
+  if constexpr (ONE) {
+    (void)it;
+    if (nmy >= 1) {
+      qk_softmax(A, tile0);
+      pv(A);
+    }
+  } else if constexpr (DT == KV_Q8) {
     {
       const int tb = nmy > 1 ? tile0 + NW : (tile0 < t_end ? tile0 : t_end - 1);
       load_tile<D, DT, QUARTER, PR>(B, tb * 32, g, n, kbase, vbase, ksb, vsb);
@@ -944,8 +952,16 @@ bool decode_plan(const LayerView& L, int S, int H, int pos_base, int num_cus, in
   tps = tps < s.waves ? s.waves : tps;
   const int tps_min = (s.n_tiles + kMaxSplits - 1) / kMaxSplits;
   tps = tps < tps_min ? tps_min : tps;
-  int ns = (s.n_tiles + tps - 1) / tps;
   const long resident = (long)(resident_per_cu > 0 ? resident_per_cu : 1) * cus;
+  // a q8 4-wave single-set plan whose waves would take two tiles at one workgroup a CU takes one
+  // tile a wave instead when a CU holds two workgroups and the GPU holds the larger grid (q8
+  // tiles cost more compute per byte, so two tiles in series on one wave cost more than a CU
+  // running two workgroups; measured slower for f16)
+  if (L.dtype == KV_Q8 && s.waves == 4 && s.nset == 1 && resident_per_cu >= 2 && tps > s.waves && tps <= 2 * s.waves) {
+    const int ns1 = (s.n_tiles + s.waves - 1) / s.waves;
+    if (ns1 <= kMaxSplits && (long)ns1 * L.kv_heads <= resident) tps = s.waves;
+  }
+  int ns = (s.n_tiles + tps - 1) / tps;
   const int max_splits = (int)(resident / L.kv_heads);
   if (max_splits < 2) {
     tps = s.n_tiles;
@@ -963,15 +979,29 @@ bool decode_plan(const LayerView& L, int S, int H, int pos_base, int num_cus, in
   return true;
 }
 
+static std::mutex g_decode_fn_mu;
+
+// dynamic LDS past 64 KB must be allowed per kernel before a launch (and before an occupancy
+// query counts it); the allowance only ever grows. Caller holds g_decode_fn_mu.
+static hipError_t allow_lds_locked(const void* fn, size_t smem) {
+  static std::map<const void*, size_t> allowed;
+  if (smem <= 64 * 1024) return hipSuccess;
+  size_t& a = allowed[fn];
+  if (smem <= a) return hipSuccess;
+  const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+  if (e == hipSuccess) a = smem;
+  return e;
+}
+
 // workgroups of one decode instantiation that fit a CU at once with `smem` bytes of dynamic
 // LDS (cached per kernel and size)
 static int resident_blocks(const void* fn, int threads, size_t smem) {
-  static std::mutex mu;
   static std::map<std::pair<const void*, size_t>, int> memo;
-  std::lock_guard<std::mutex> lock(mu);
+  std::lock_guard<std::mutex> lock(g_decode_fn_mu);
   auto it = memo.find({fn, smem});
   if (it != memo.end()) return it->second;
   int nb = 0;
+  if (allow_lds_locked(fn, smem) != hipSuccess) (void)hipGetLastError();
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fn, threads, smem) != hipSuccess || nb < 1) {
     (void)hipGetLastError();
     nb = 1;
@@ -999,10 +1029,10 @@ size_t decode_workspace_floats(const LayerView& L, int S, int H, int num_cus, si
   return (size_t)L.kv_heads * R * (L.D / 64) * ns_max * kUnitF4 * 4;
 }
 
-template <int D, int DT, bool ROLL, int NSET, int NPT, int NW, int PR>
+template <int D, int DT, bool ROLL, int NSET, int NPT, int NW, int PR, bool ONE = false>
 static hipError_t launch_cfg(const LayerView& L, const AttnArgs& a, hipStream_t st) {
   using SM = DecodeSmem<D, DT, ROLL, NSET, NW, PR>;
-  const void* fn = (const void*)decode_kernel<D, DT, ROLL, NSET, NW, NPT, PR>;
+  const void* fn = (const void*)decode_kernel<D, DT, ROLL, NSET, NW, NPT, PR, ONE>;
   const int R = (a.H / L.kv_heads) * a.S;
   if (rows_per_pass(R) != PR) return hipErrorInvalidValue;
   const int NP = (R + PR - 1) / PR;
@@ -1012,17 +1042,16 @@ static hipError_t launch_cfg(const LayerView& L, const AttnArgs& a, hipStream_t 
   const size_t merge_max = (((size_t)kMaxSplits * 4 + 15) & ~(size_t)15) + (size_t)NW * 16 * 16;
   smem = smem > merge_max ? smem : merge_max;
   if (smem > kDecodeLdsMax) return hipErrorInvalidValue;
-  if (smem > 64 * 1024) {
-    static size_t attr_bytes = 0;
-    if (smem > attr_bytes) {
-      hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
-      if (e != hipSuccess) return e;
-      attr_bytes = smem;
-    }
+  {
+    std::lock_guard<std::mutex> lock(g_decode_fn_mu);
+    const hipError_t e = allow_lds_locked(fn, smem);
+    if (e != hipSuccess) return e;
   }
   DecodePlan sp;
   if (!decode_plan(L, a.S, a.H, a.pos_base, a.num_cus, resident_blocks(fn, 64 * NW, smem), &sp)) return hipErrorInvalidValue;
   if (sp.waves != NW || sp.nset != NSET || (NPT > 0 && sp.passes != NPT)) return hipErrorInvalidValue;
+  if (ONE && sp.n_splits > 1 && sp.tiles_per_split > NW) return hipErrorInvalidValue;  // a wave with two tiles
+  if (ONE && sp.n_splits == 1 && sp.n_tiles > NW) return hipErrorInvalidValue;
   DecodeParams p;
   p.L = L;
   p.q = a.q;
@@ -1049,7 +1078,7 @@ static hipError_t launch_cfg(const LayerView& L, const AttnArgs& a, hipStream_t 
   p.err = a.err;
   p.spin_limit = a.spin_limit > 0 ? a.spin_limit : (1 << 20);
   p.withhold_split = a.withhold_split;
-  hipLaunchKernelGGL((decode_kernel<D, DT, ROLL, NSET, NW, NPT, PR>), dim3(sp.grid), dim3(64 * NW), smem, st, p);
+  hipLaunchKernelGGL((decode_kernel<D, DT, ROLL, NSET, NW, NPT, PR, ONE>), dim3(sp.grid), dim3(64 * NW), smem, st, p);
   return hipGetLastError();
 }
 
@@ -1069,6 +1098,22 @@ static hipError_t launch_nset(const LayerView& L, const AttnArgs& a, int nset, h
           if (np == 1) return launch_cfg<D, DT, ROLL, 1, 1, 8, 8>(L, a, st);
           return launch_cfg<D, DT, ROLL, 1, 2, 8, 8>(L, a, st);
         }
+      }
+      // q8: one tile a wave when the plan for the one-tile kernel's residency gives it (the
+      // two-tile kernel's prefetch would re-read the wave's only tile)
+      if constexpr (DT == KV_Q8) {
+        auto one_tile = [&](const void* fn, int pr) {
+          const size_t smem = std::max(decode_lds_bytes(D, DT, R, 4, pr), (((size_t)kMaxSplits * 4 + 15) & ~(size_t)15) + 4 * 16 * 16);
+          DecodePlan p1;
+          return decode_plan(L, a.S, a.H, a.pos_base, a.num_cus, resident_blocks(fn, 256, smem), &p1) &&
+                 p1.waves == 4 && (p1.n_splits > 1 ? p1.tiles_per_split == 4 : p1.n_tiles <= 4);
+        };
+        if (R <= 4 && one_tile((const void*)decode_kernel<D, DT, ROLL, 1, 4, 1, 4, true>, 4))
+          return launch_cfg<D, DT, ROLL, 1, 1, 4, 4, true>(L, a, st);
+        if (R > 4 && np == 1 && one_tile((const void*)decode_kernel<D, DT, ROLL, 1, 4, 1, 8, true>, 8))
+          return launch_cfg<D, DT, ROLL, 1, 1, 4, 8, true>(L, a, st);
+        if (R > 4 && np == 2 && one_tile((const void*)decode_kernel<D, DT, ROLL, 1, 4, 2, 8, true>, 8))
+          return launch_cfg<D, DT, ROLL, 1, 2, 4, 8, true>(L, a, st);
       }
       if (R <= 4) return launch_cfg<D, DT, ROLL, 1, 1, 4, 4>(L, a, st);
       if (np == 1) return launch_cfg<D, DT, ROLL, 1, 1, 4, 8>(L, a, st);
