@@ -91,6 +91,9 @@ int32_t bg_stream_sync(void* stream);
  * BG_KV_Q8), on num_cus CUs holding resident_per_cu of its workgroups at once. out[0..5] =
  * waves per workgroup, splits per kv head, 32-slot tiles per split, merging splits per kv
  * head (the last ones), grid size, tiles. The grid never exceeds resident_per_cu * num_cus.
+ * A q8 launch of 4-wave workgroups whose waves would take two tiles at one workgroup a CU takes
+ * one tile a wave when resident_per_cu >= 2 and the GPU holds that grid (bg_attention runs a
+ * one-tile kernel that fits two workgroups a CU there).
  * BG_E_UNSUPPORTED when the shape goes to another kernel. */
 int32_t bg_decode_plan(int32_t kv_heads, int32_t head_dim, int32_t dtype, int32_t S, int32_t H,
                        int32_t pos_base, int32_t num_cus, int32_t resident_per_cu, int32_t* out);

@@ -222,6 +222,22 @@ def test_decode_plan_residency_cap():
     assert _plan(8, 128, 64, 32, 1000)[0] == _lib.BG_E_UNSUPPORTED
 
 
+def test_decode_plan_one_tile_rule():
+    """q8, 4-wave single-set launches: when one workgroup a CU would leave waves with two tiles
+    and a CU holds two workgroups, the plan gives every wave one tile on a larger grid."""
+    # C5 decode: 257 tiles x 4 kv heads (8193 positions) on 256 CUs
+    rc, (waves, ns, tps, nm, grid, tiles) = _plan(4, 256, 1, 24, 8192, 256, 1)
+    assert rc == 0 and (waves, tps, ns, grid) == (4, 5, 52, 208)      # one a CU: one wave has two tiles
+    rc, (waves, ns, tps, nm, grid, tiles) = _plan(4, 256, 1, 24, 8192, 256, 2)
+    assert rc == 0 and (waves, tps, ns, grid) == (4, 4, 65, 260)      # two a CU: one tile a wave
+    assert nm == min(6 * 4, 65)
+    # f16 keeps one workgroup a CU (measured faster), and so does a GPU that cannot hold the grid
+    assert _plan(4, 256, 1, 24, 8192, 256, 2, dtype=_lib.BG_KV_F16)[1][2] == 5
+    assert _plan(4, 256, 1, 24, 8192, 128, 2)[1][2] == 9
+    # more than two tiles a wave at one workgroup a CU: unchanged
+    assert _plan(4, 256, 1, 24, 3 * 8192, 256, 2)[1][2] == 13
+
+
 # ---------------------------------------------------------------- 1-bit projections: host checks
 def test_gemv_argument_validation():
     lib = _lib.lib()
