@@ -450,6 +450,41 @@ def bench_projections(torch, E, steps, warmup, layers=36, HD=4096, H=32, KV=8, D
             "shape": f"hidden {HD}, {H} heads / {KV} kv heads x {D}, {layers} distinct layers"}
 
 
+def bench_read_floor(torch, steps, warmup, layers=36, nbytes=None, grids=(256, 512, 1024, 2048)):
+    """The streaming-read floor of the headline's traffic: `layers` distinct buffers of the C3
+    32k layer's algorithmic bytes, each read by one bg_diag_stream_read launch (512-thread
+    workgroups, one contiguous slice each, 16-byte loads), graph-replayed like the headline
+    sweep. Nontemporal loads (the decode tiles' policy) at each grid size; the best grid is
+    also timed with plain loads."""
+    import ctypes as C
+    from bitgpu_amd._lib import check, lib
+    nbytes = nbytes or c3_bytes(32768)
+    bufs = [torch.randint(-2 ** 31, 2 ** 31 - 1, (nbytes // 4,), dtype=torch.int32, device="cuda")
+            for _ in range(layers)]
+    sink = torch.empty(max(grids), dtype=torch.int32, device="cuda")
+
+    def timed(wg, nt):
+        def sweep():
+            st = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+            for b in bufs:
+                check(lib().bg_diag_stream_read(C.c_void_p(b.data_ptr()), nbytes, wg, nt, C.c_void_p(sink.data_ptr()),
+                                                st))
+        return graph_replay_us(torch, sweep, steps, warmup) / layers
+
+    def entry(us):
+        return {"us_per_launch": round(us, 2), "GBs": round(nbytes / us / 1e3, 1),
+                "hbm_frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+
+    per_grid = {wg: timed(wg, 1) for wg in grids}
+    best = min(per_grid, key=per_grid.get)
+    out = {"bytes_per_launch": nbytes, "buffers": layers,
+           "nontemporal_by_grid": {str(wg): round(us, 2) for wg, us in per_grid.items()},
+           "best_grid": best, "nontemporal": entry(per_grid[best]), "plain": entry(timed(best, 0))}
+    del bufs
+    torch.cuda.empty_cache()
+    return out
+
+
 def load_traffic(name):
     p = os.path.join(ROOT, "profiles", name)
     if not os.path.exists(p):
@@ -476,6 +511,8 @@ def main():
                          "kernels --profile-n times each (for rocprofv3 --pmc), print nothing else")
     ap.add_argument("--profile-n", type=int, default=20)
     ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--read-floor", action="store_true",
+                    help="run only the streaming-read floor of the headline's bytes and print it as JSON")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="run only a device-to-device copy of MIB MiB (3 times) to calibrate the "
                          "FETCH_SIZE / WRITE_SIZE counters against known bytes")
@@ -505,6 +542,10 @@ def main():
 
     if args.profile_prefill:
         profile_prefill(torch, E, W, args.profile_prefill)
+        return
+
+    if args.read_floor:
+        print(json.dumps({"read_floor_c3_32k": bench_read_floor(torch, args.steps, args.warmup)}), flush=True)
         return
 
     if args.profile_set:
@@ -544,6 +585,7 @@ def main():
         extra["c1_decode_f32"] = bench_c1(torch, E, W, args.steps, args.warmup)
         extra["c4_sinks_f16"] = bench_c4(torch, E, W, args.steps, args.warmup)
         extra["projections_1bit"] = bench_projections(torch, E, args.steps, args.warmup)
+        extra["read_floor_c3_32k"] = bench_read_floor(torch, args.steps, args.warmup)
         cpu = cpu_baseline(sweep, W, args.cpu_budget)
     sweep.close()
 

@@ -972,6 +972,14 @@ int32_t bg_decode_plan(int32_t kv_heads, int32_t head_dim, int32_t dtype, int32_
   return BG_OK;
 }
 
+int32_t bg_diag_stream_read(const void* buf, size_t bytes, int32_t workgroups, int32_t nontemporal, uint32_t* sink,
+                            void* stream) {
+  if (!buf || !sink || bytes == 0 || bytes % 16 || workgroups < 1 || workgroups > 65535)
+    return fail(BG_E_INVALID, "bg_diag_stream_read: bad arguments (bytes %zu, workgroups %d)", bytes, workgroups);
+  const hipError_t e = bg::launch_stream_read(buf, bytes, workgroups, nontemporal != 0, sink, (hipStream_t)stream);
+  return e == hipSuccess ? BG_OK : hip_fail(e, "bg_diag_stream_read");
+}
+
 int32_t bg_kv_ring_reset(bg_kv_cache* c, int64_t evicted) {
   if (!c) return fail(BG_E_INVALID, "bg_kv_ring_reset: NULL cache");
   if (!c->roll) return fail(BG_E_STATE, "bg_kv_ring_reset: cache is not in sink mode");

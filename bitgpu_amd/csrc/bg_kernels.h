@@ -120,6 +120,10 @@ struct DecodePlan {
   int tiles_per_split, n_splits, n_mergers, grid;
 };
 bool decode_plan(const LayerView& L, int S, int H, int pos_base, int num_cus, int resident_per_cu, DecodePlan* out);
+// streaming-read floor (diag.hip): `workgroups` contiguous slices of `bytes` read with 16-byte
+// loads, one XOR word per workgroup into sink
+hipError_t launch_stream_read(const void* buf, size_t bytes, int workgroups, bool nontemporal, unsigned* sink,
+                              hipStream_t st);
 bool prefill_supported(const LayerView& L, int S, int H);
 // a q8 prefill of S rows that stages each K/V tile for enough query blocks to run faster on an
 // f16 copy of the attended slots

@@ -98,6 +98,15 @@ int32_t bg_stream_sync(void* stream);
 int32_t bg_decode_plan(int32_t kv_heads, int32_t head_dim, int32_t dtype, int32_t S, int32_t H,
                        int32_t pos_base, int32_t num_cus, int32_t resident_per_cu, int32_t* out);
 
+/* Measurement aid with no counterpart in the reference: the streaming-read floor the decode
+ * kernels are held against. `workgroups` workgroups of 512 threads each read one contiguous
+ * slice of the device buffer `buf` (`bytes`, a multiple of 16) with 16-byte loads, eight in
+ * flight a lane, nontemporal (the decode tiles' policy) or plain, and fold them by XOR into
+ * sink[workgroup] (device memory, `workgroups` words). The XOR of the sink words equals the XOR
+ * of the buffer's 32-bit words. Asynchronous on `stream`; allocates nothing. */
+int32_t bg_diag_stream_read(const void* buf, size_t bytes, int32_t workgroups, int32_t nontemporal,
+                            uint32_t* sink, void* stream);
+
 /* ---- streams and event timing -------------------------------------------------------------
  * For hosts without a GPU runtime of their own (the N-API addon): the reference runs every
  * dispatch on its one WebGPU queue and times with timestamp queries (src/engine.ts:503-506);

@@ -222,6 +222,18 @@ def test_decode_plan_residency_cap():
     assert _plan(8, 128, 64, 32, 1000)[0] == _lib.BG_E_UNSUPPORTED
 
 
+def test_diag_stream_read_argument_validation():
+    lib = _lib.lib()
+    buf = (C.c_uint32 * 64)()
+    p = C.cast(buf, C.c_void_p)
+    assert lib.bg_diag_stream_read(p, 100, 4, 1, p, None) == _lib.BG_E_INVALID       # not a multiple of 16
+    assert b"bg_diag_stream_read" in lib.bg_last_error_message()
+    assert lib.bg_diag_stream_read(None, 256, 4, 1, p, None) == _lib.BG_E_INVALID
+    assert lib.bg_diag_stream_read(p, 256, 4, 1, None, None) == _lib.BG_E_INVALID
+    assert lib.bg_diag_stream_read(p, 256, 0, 1, p, None) == _lib.BG_E_INVALID
+    assert lib.bg_diag_stream_read(p, 0, 4, 1, p, None) == _lib.BG_E_INVALID
+
+
 def test_decode_plan_one_tile_rule():
     """q8, 4-wave single-set launches: when one workgroup a CU would leave waves with two tiles
     and a CU holds two workgroups, the plan gives every wave one tile on a larger grid."""
