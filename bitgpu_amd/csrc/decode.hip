@@ -8,12 +8,17 @@
 //           a range of 32-slot tiles; its waves take every NW-th tile. All R = (H/KV)*S query rows of the
 //           GQA group are served by one read of each K/V byte.
 //   QK    = v_mfma_f32_16x16x32_f16 with K as the B operand (lane = slot, 8 dims per lane
-//           group) and a block-diagonal Q as A: row group g of the 16 output rows only sees the
-//           dims lane group g loaded, so the MFMA returns 4 partial dot products per slot that
-//           three permlane swaps reduce-scatter into one full score per lane -- no padding rows.
-//           q8 codes enter the MFMA as exact f16 integers (xor/perm/pk_add, no float convert);
-//           the per-32 block scale multiplies the MFMA result. Q is split hi+lo f16 so the
-//           product keeps ~f32 accuracy.
+//           group) and a block-diagonal Q as A, in passes of 4 or 8 query rows: with 4, row
+//           group g of the 16 output rows only sees the dims lane group g loaded, so the MFMA
+//           returns 4 partial dot products per slot that three permlane swaps reduce-scatter
+//           into one full score per lane; with 8 (more than 4 rows per kv head), each half of
+//           the output rows sees two lane groups and one swap per pair of rows leaves two full
+//           scores per lane. q8 codes enter the MFMA as exact f16 integers (xor/perm/pk_add,
+//           no float convert); the per-32 block scale multiplies the MFMA result. Q is split
+//           hi+lo f16 so the product keeps ~f32 accuracy.
+//   tiles = each wave keeps two 32-slot tiles in flight in registers; q8 launches whose plan
+//           gives every wave one tile run a one-tile variant (half the registers: two
+//           workgroups a CU).
 //   softmax = online, base 2, per 32-slot tile; probabilities (times the q8 V block scale) go
 //           through a 2 KB-per-block LDS transpose into the B operand of
 //   PV    = v_mfma_f32_16x16x32_f16 with V^T (the cache's transposed V tile, 16 B per lane)
