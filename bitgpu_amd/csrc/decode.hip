@@ -124,6 +124,11 @@ struct DecodeParams {
   unsigned* err;       // host-visible error word: a merger's bounded wait gave up
   int spin_limit;      // poll rounds before a merger gives up
   int withhold_split;  // test hook: this split stores no partial (-1: none)
+  // > 0: workgroups numbered in groups of xcd_group consecutive splits per kv head, so the kv
+  // heads of one split share blockIdx mod 8 (one XCD when workgroups go to XCDs round robin):
+  // sink mode's cos/sin rows of a slot are then fetched into one L2 for all kv heads. The last
+  // group is padded; its padding workgroups exit at once.
+  int xcd_group;
 };
 
 // "not written yet" marker of a partial slot: a quiet NaN with a payload that arithmetic on
@@ -271,8 +276,16 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
   const int lane = tid & 63;
   const int g = lane >> 4;      // lane group
   const int n = lane & 15;
-  const int kvh = blockIdx.x % p.L.kv_heads;
-  const int split = blockIdx.x / p.L.kv_heads;
+  int kvh, split;
+  if (p.xcd_group > 0) {
+    const int span = p.xcd_group * p.L.kv_heads, r = blockIdx.x % span;
+    kvh = r / p.xcd_group;
+    split = (blockIdx.x / span) * p.xcd_group + r % p.xcd_group;
+  } else {
+    kvh = blockIdx.x % p.L.kv_heads;
+    split = blockIdx.x / p.L.kv_heads;
+  }
+  if (split >= p.n_splits) return;  // padding of the last split group (the whole workgroup)
   const int NP = NPT > 0 ? NPT : (p.R + PR - 1) / PR;
   // query row of pass `pass` that lane group g holds in slot i (i < RL) after the reduction
   auto row_of = [&](int pass, int i) { return PR == 4 ? 4 * pass + g : 8 * pass + 2 * i + (g >> 1) + 4 * (g & 1); };
@@ -980,6 +993,17 @@ bool decode_plan(const LayerView& L, int S, int H, int pos_base, int num_cus, in
   const int units = R * (L.D / 64);  // merge units: one row x 64 dims
   s.n_mergers = ns > 1 ? (units < ns ? units : ns) : 0;
   s.grid = ns * L.kv_heads;
+  s.xcd_group = 0;
+  // sink mode: number the splits in groups of 8 so that the kv heads of a split share an XCD's
+  // L2 for the slots' cos/sin rows (per kv head split k keeps a higher index than split j < k, so
+  // the mergers are still dispatched after every split they wait on)
+  if (L.ring.roll && ns > 1 && L.kv_heads > 1) {
+    const long padded = (long)((ns + 7) / 8) * 8 * L.kv_heads;
+    if (padded <= resident) {
+      s.xcd_group = 8;
+      s.grid = (int)padded;
+    }
+  }
   *out = s;
   return true;
 }
@@ -1083,6 +1107,7 @@ static hipError_t launch_cfg(const LayerView& L, const AttnArgs& a, hipStream_t 
   p.err = a.err;
   p.spin_limit = a.spin_limit > 0 ? a.spin_limit : (1 << 20);
   p.withhold_split = a.withhold_split;
+  p.xcd_group = sp.xcd_group;
   hipLaunchKernelGGL((decode_kernel<D, DT, ROLL, NSET, NW, NPT, PR, ONE>), dim3(sp.grid), dim3(64 * NW), smem, st, p);
   return hipGetLastError();
 }
