@@ -292,7 +292,7 @@ def test_q8_per_row_scale_mode(dev, D):
     ek, ev, eks, evs = export_k_v(c, 0, 0, L)
     assert np.array_equal(ek, ref.q8_pack(k, block=D)[0]) and np.array_equal(ev, ref.q8_pack(v, block=D)[0])
     kk, vv = ref.q8_dequant(ek, eks), ref.q8_dequant(ev, evs)
-    for S in (1, 300):
+    for S in (1, 2, 3, 300):   # decode passes of 4 and 8 rows (one and two), prefill
         q = rng.standard_normal((S, H, D)).astype(np.float32)
         out = run_attention(c, 0, q, L - S)
         exp = ref.attention(q, kk, vv, L - S)
