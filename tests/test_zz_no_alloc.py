@@ -70,6 +70,33 @@ def test_noalloc_matches_bg_attention(dev, dtype, H, KV, D, L, calls, gated):
     c.close()
 
 
+@pytest.mark.parametrize("dtype", ["f16", "q8"])
+def test_noalloc_matches_bg_attention_sink_ring(dev, dtype):
+    """Sink mode with the ring wrapped (read-time rotation, splits numbered in groups per kv head):
+    decode and a 5-row verify, bit-identical to bg_attention, twice each."""
+    KV, H, D, sinks, window = 8, 32, 128, 4, 700
+    max_seq = sinks + window
+    c = E.KvCache(1, KV, D, dtype, max_seq_len=max_seq, overflow="sinks", sink_tokens=sinks)
+    cos_d, sin_d, _, _ = rope_dev(1e6, D, max_seq)
+    c.set_rope(cos_d, sin_d)
+    rng = np.random.default_rng(91)
+    fill_cache_raw(c, 0, rng.standard_normal((max_seq, KV, D)).astype(np.float32),
+                   rng.standard_normal((max_seq, KV, D)).astype(np.float32))
+    fill, fed = 500, 500
+    while fed < 3000:
+        fill = c.evict_for(fill, 4) + 4
+        fed += 4
+    for S in (1, 5, 1):
+        fill = c.evict_for(fill, S)
+        assert c.ring_state()[0] != 0
+        q = t(rng.standard_normal((S, H, D)).astype(np.float32))
+        want = E.attention(c, 0, q, S, H, fill)
+        got = _noalloc(c, 0, q, S, H, fill)
+        torch.cuda.synchronize()
+        assert torch.isfinite(got).all() and torch.equal(got, want)
+    c.close()
+
+
 def test_noalloc_rejects_partials_beyond_the_scratch(dev):
     # 200 kv heads x 48 rows x 2 splits of decode partials = 10.4 MB > the 8 MiB scratch (a
     # sink-mode cache: its 48-row verify stays on the decode kernel)
