@@ -10,17 +10,24 @@
 // f32 scale [n][k / 128] (shaders/matmul_split_sg.wgsl:24-35).
 //
 //   rows    a wave computes kGemvRW output rows; a lane owns one 32-weight word of each row per
-//           2048-weight tile of K and the 32 x values under it (eight 16-byte loads, reused by the
-//           wave's rows). The word's signs flip the x values' sign bits (one xor each), four
-//           partial sums per word, times the word's block scale; a DPP / permlane wave sum
-//           finishes the row. Two tiles' loads (the rows' words and scales, x) are in flight:
-//           the next tile is issued before the current one's arithmetic; the residual is
-//           loaded at the start.
+//           2048-weight tile of K. Rows up to kLutMaxK long (the Qwen3-8B qkv and o_proj): the
+//           workgroup first tabulates, for every word of x and each of its 8 nibbles, the 16
+//           signed sums of the nibble's 4 x values (64 KB of LDS at K = 4096); a word's signed sum
+//           is then 8 table reads (indexed by the word's nibbles) and 7 adds instead of 32
+//           sign flips and adds. Longer rows: the lane holds the 32 x values under its word
+//           (eight 16-byte loads from LDS or memory, reused by the wave's rows) and the word's
+//           signs flip their sign bits (one xor each), four partial sums per word. Either way
+//           times the word's block scale; a DPP / permlane wave sum finishes the row. Two tiles'
+//           loads (the rows' words and scales, x) are in flight: the next tile is issued before
+//           the current one's arithmetic; the residual is loaded at the start.
 //   fused   the qkv kernel's workgroups own 16 rows of one head; each stores its raw rows (Q
 //           into q_out, K and V into the cache's small raw buffer), and the last workgroup of a
 //           head to arrive (an arrival counter per head, reset by that workgroup) normalizes
 //           and ropes the head (Q -> q_out; K -> the cache row, unroped in sink mode) or stores
 //           it (V), with the fused prologue's row arithmetic (bg_qkrow.h).
+#include <map>
+#include <mutex>
+
 #include "bg_kernels.h"
 #include "bg_qkrow.h"
 
@@ -42,6 +49,31 @@ struct GemvTile {
 constexpr int kXPad = 36;
 constexpr int kGemvLdsMaxK = 12288;  // 54 KB of LDS; longer rows read x from global memory
 
+// Where a lane finds the x values under its words: kXGlobal (memory), kXLds (x staged in LDS),
+// kXLut (the nibble table below; K <= kLutMaxK)
+constexpr int kXGlobal = 0, kXLds = 1, kXLut = 2;
+constexpr int kLutMaxK = 4096;  // 16 K bytes of LDS: 64 KB at the limit
+
+__host__ __device__ constexpr size_t gemv_lut_bytes(int K) { return (size_t)K * 16; }
+
+// The nibble table: lut[(16 g + e) W + w] = sum over k < 4 of (bit k of e set ? +x : -x) of
+// x[32 w + 4 g + k], summed as (k0, k1) + (k2, k3): every signed combination of a nibble's four
+// x values (bit set = weight +1, as in the word loop). W-fastest, so the lanes' reads (one word
+// each) fall on distinct banks. The whole workgroup builds it, then a barrier.
+__device__ __forceinline__ void gemv_build_lut(const float* __restrict__ x, float* lut, int K) {
+  const int W = K >> 5;
+  for (int i = threadIdx.x; i < 8 * W; i += blockDim.x) {
+    const int w = i % W, g = i / W;
+    const float4 v = *(const float4*)(x + 32 * w + 4 * g);
+    const float a[4] = {-v.x - v.y, v.x - v.y, v.y - v.x, v.x + v.y};
+    const float b[4] = {-v.z - v.w, v.z - v.w, v.w - v.z, v.z + v.w};
+    float* d = lut + (size_t)(16 * g) * W + w;
+#pragma unroll
+    for (int e = 0; e < 16; e++) d[(size_t)e * W] = a[e & 3] + b[e >> 2];
+  }
+  __syncthreads();
+}
+
 template <int RW>
 __device__ __forceinline__ void gemv_load_w(GemvTile<RW>& T, int W, int NB, const uint32_t* __restrict__ sign,
                                             const float* __restrict__ scales, int n0, int n_rows, int t, int lane) {
@@ -56,15 +88,16 @@ __device__ __forceinline__ void gemv_load_w(GemvTile<RW>& T, int W, int NB, cons
   }
 }
 
-template <int RW, bool XLDS>
+template <int RW, int XM>
 __device__ __forceinline__ void gemv_load_x(GemvTile<RW>& T, const float* __restrict__ x, const float* xs, int W, int t,
                                             int lane) {
+  if constexpr (XM == kXLut) return;  // the table holds x
   const int w = 64 * t + lane;
   const bool ok = w < W;
 #pragma unroll
   for (int j = 0; j < 8; j++) {
     float4 f;
-    if constexpr (XLDS) f = ok ? *(const float4*)(xs + kXPad * w + 4 * j) : make_float4(0.f, 0.f, 0.f, 0.f);
+    if constexpr (XM == kXLds) f = ok ? *(const float4*)(xs + kXPad * w + 4 * j) : make_float4(0.f, 0.f, 0.f, 0.f);
     else f = ok ? *(const float4*)(x + 32 * w + 4 * j) : make_float4(0.f, 0.f, 0.f, 0.f);
     T.xv[4 * j] = f.x;
     T.xv[4 * j + 1] = f.y;
@@ -73,12 +106,12 @@ __device__ __forceinline__ void gemv_load_x(GemvTile<RW>& T, const float* __rest
   }
 }
 
-template <int RW, bool XLDS>
+template <int RW, int XM>
 __device__ __forceinline__ void gemv_load(GemvTile<RW>& T, const float* __restrict__ x, const float* xs, int W, int NB,
                                           const uint32_t* __restrict__ sign, const float* __restrict__ scales,
                                           int n0, int n_rows, int t, int lane) {
   gemv_load_w<RW>(T, W, NB, sign, scales, n0, n_rows, t, lane);
-  gemv_load_x<RW, XLDS>(T, x, xs, W, t, lane);
+  gemv_load_x<RW, XM>(T, x, xs, W, t, lane);
 }
 
 // stage x[K] into xs (the whole workgroup, coalesced 16-byte loads), then a barrier
@@ -90,9 +123,27 @@ __device__ __forceinline__ void gemv_stage_x(const float* __restrict__ x, float*
   __syncthreads();
 }
 
-template <int RW>
-__device__ __forceinline__ void gemv_accumulate(const GemvTile<RW>& T, float (&acc)[RW], int lane) {
-  (void)lane;
+template <int RW, int XM>
+__device__ __forceinline__ void gemv_accumulate(const GemvTile<RW>& T, float (&acc)[RW], const float* lut, int W, int t,
+                                                int lane) {
+  if constexpr (XM == kXLut) {
+    // a lane past the last word reads word W-1's entries, weighted by its zero scale; entry
+    // (g, e) of the lane's word at byte (16 g + e) 4W + 4w (24-bit products: the table is 64 KB)
+    const int w = min(64 * t + lane, W - 1);
+    const unsigned W4 = 4u * (unsigned)W;
+    const char* rowg[8];
+#pragma unroll
+    for (int g = 0; g < 8; g++) rowg[g] = (const char*)lut + 4 * w + __umul24(16u * g, W4);
+#pragma unroll
+    for (int r = 0; r < RW; r++) {
+      const uint32_t wd = T.word[r];
+      float l[8];
+#pragma unroll
+      for (int g = 0; g < 8; g++) l[g] = *(const float*)(rowg[g] + __umul24(__builtin_amdgcn_ubfe(wd, 4 * g, 4), W4));
+      acc[r] = fmaf(((l[0] + l[1]) + (l[2] + l[3])) + ((l[4] + l[5]) + (l[6] + l[7])), T.sc[r], acc[r]);
+    }
+    return;
+  }
 #pragma unroll
   for (int r = 0; r < RW; r++) {
     // clear bit i -> weight -1: flip the sign bit of x_i
@@ -107,8 +158,9 @@ __device__ __forceinline__ void gemv_accumulate(const GemvTile<RW>& T, float (&a
 // totals of rows n0 .. n0 + RW - 1 (rows >= n_rows give 0); every lane holds every total. Two
 // tiles are in flight: the next tile's loads are issued before the current tile's arithmetic
 // (a uniform trip count, so the compiler keeps them outstanding across the loop head).
-// (the caller issues tile 0's weight loads into A, then stages x when XLDS, then calls this)
-template <int RW, bool XLDS>
+// (the caller issues tile 0's weight loads into A, then stages x or builds the table, then calls
+// this; xs is the staged x or the table)
+template <int RW, int XM>
 __device__ inline void gemv_rows(GemvTile<RW>& A, const float* __restrict__ x, const float* xs, int K,
                                  const uint32_t* __restrict__ sign, const float* __restrict__ scales, int n0, int n_rows,
                                  int lane, float (&tot)[RW]) {
@@ -118,20 +170,20 @@ __device__ inline void gemv_rows(GemvTile<RW>& A, const float* __restrict__ x, c
 #pragma unroll
   for (int r = 0; r < RW; r++) acc[r] = 0.0f;
   GemvTile<RW> B;
-  gemv_load_x<RW, XLDS>(A, x, xs, W, 0, lane);
+  gemv_load_x<RW, XM>(A, x, xs, W, 0, lane);
   int t = 0;
   for (; t + 2 <= n_tiles; t += 2) {
-    gemv_load<RW, XLDS>(B, x, xs, W, NB, sign, scales, n0, n_rows, t + 1, lane);
-    gemv_accumulate<RW>(A, acc, lane);
-    if (t + 2 < n_tiles) gemv_load<RW, XLDS>(A, x, xs, W, NB, sign, scales, n0, n_rows, t + 2, lane);
-    gemv_accumulate<RW>(B, acc, lane);
+    gemv_load<RW, XM>(B, x, xs, W, NB, sign, scales, n0, n_rows, t + 1, lane);
+    gemv_accumulate<RW, XM>(A, acc, xs, W, t, lane);
+    if (t + 2 < n_tiles) gemv_load<RW, XM>(A, x, xs, W, NB, sign, scales, n0, n_rows, t + 2, lane);
+    gemv_accumulate<RW, XM>(B, acc, xs, W, t + 1, lane);
   }
-  if (t < n_tiles) gemv_accumulate<RW>(A, acc, lane);
+  if (t < n_tiles) gemv_accumulate<RW, XM>(A, acc, xs, W, t, lane);
 #pragma unroll
   for (int r = 0; r < RW; r++) tot[r] = wave_sum(acc[r]);
 }
 
-template <bool XLDS>
+template <int XM>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   extern __shared__ __align__(16) float xs[];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -142,10 +194,11 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   const float res = (a.resid && lane < kGemvRW && n0 + lane < N) ? a.resid[n0 + lane] : 0.0f;
   GemvTile<kGemvRW> A;
   gemv_load_w<kGemvRW>(A, a.K >> 5, a.K >> 7, a.sign, a.scales, n0, N, 0, lane);
-  if constexpr (XLDS) gemv_stage_x(a.x, xs, a.K);
+  if constexpr (XM == kXLds) gemv_stage_x(a.x, xs, a.K);
+  if constexpr (XM == kXLut) gemv_build_lut(a.x, xs, a.K);
   if (n0 >= N) return;  // wave-uniform
   float tot[kGemvRW];
-  gemv_rows<kGemvRW, XLDS>(A, a.x, xs, a.K, a.sign, a.scales, n0, N, lane, tot);
+  gemv_rows<kGemvRW, XM>(A, a.x, xs, a.K, a.sign, a.scales, n0, N, lane, tot);
 #pragma unroll
   for (int r = 0; r < kGemvRW; r++) {
     const int n = n0 + r;
@@ -158,15 +211,34 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   }
 }
 
+// the LDS a kernel may take beyond the default (at most 64 KB of table plus a few static arrays),
+// set once per kernel
+static hipError_t gemv_allow_lds(const void* fn, size_t bytes) {
+  static std::mutex mu;
+  static std::map<const void*, size_t> allowed;
+  std::lock_guard<std::mutex> lock(mu);
+  size_t& a = allowed[fn];
+  if (bytes <= a) return hipSuccess;
+  const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+  if (e == hipSuccess) a = bytes;
+  return e;
+}
+
 hipError_t launch_gemv(const GemvArgs& a, hipStream_t st) {
   const int N = a.N0 + a.N1 + a.N2;
   if (N <= 0) return hipSuccess;
   const int waves = (N + kGemvRW - 1) / kGemvRW;
-  if (a.K <= kGemvLdsMaxK) {
+  const dim3 g((waves + 3) / 4);
+  if (a.K <= kLutMaxK) {
+    const size_t lds = gemv_lut_bytes(a.K);
+    const hipError_t e = gemv_allow_lds((const void*)gemv_kernel<kXLut>, lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(gemv_kernel<kXLut>, g, dim3(256), lds, st, a);
+  } else if (a.K <= kGemvLdsMaxK) {
     const size_t lds = (size_t)(a.K / 32) * kXPad * sizeof(float);
-    hipLaunchKernelGGL(gemv_kernel<true>, dim3((waves + 3) / 4), dim3(256), lds, st, a);
+    hipLaunchKernelGGL(gemv_kernel<kXLds>, g, dim3(256), lds, st, a);
   } else {
-    hipLaunchKernelGGL(gemv_kernel<false>, dim3((waves + 3) / 4), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(gemv_kernel<kXGlobal>, g, dim3(256), 0, st, a);
   }
   return hipGetLastError();
 }
@@ -174,7 +246,7 @@ hipError_t launch_gemv(const GemvArgs& a, hipStream_t st) {
 // ---- fused decode qkv projection + prologue ---------------------------------------------------
 constexpr int kQkvRowsPerWg = 4 * kGemvRW;  // 16 rows of one head
 
-template <int D, int DT, bool XLDS>
+template <int D, int DT, int XM>
 __global__ __launch_bounds__(256) void qkv_proj_kernel(LayerView L, QkvProjArgs a) {
   constexpr int LPR = D / 4;  // lanes per row in the epilogue
   extern __shared__ __align__(16) float xs[];
@@ -190,9 +262,10 @@ __global__ __launch_bounds__(256) void qkv_proj_kernel(LayerView L, QkvProjArgs 
     const int n0 = wg_n0 + wave * kGemvRW;
     GemvTile<kGemvRW> A;
     gemv_load_w<kGemvRW>(A, a.K >> 5, a.K >> 7, a.sign, a.scales, n0, N, 0, lane);
-    if constexpr (XLDS) gemv_stage_x(a.x, xs, a.K);
+    if constexpr (XM == kXLds) gemv_stage_x(a.x, xs, a.K);
+    if constexpr (XM == kXLut) gemv_build_lut(a.x, xs, a.K);
     float tot[kGemvRW];
-    gemv_rows<kGemvRW, XLDS>(A, a.x, xs, a.K, a.sign, a.scales, n0, N, lane, tot);
+    gemv_rows<kGemvRW, XM>(A, a.x, xs, a.K, a.sign, a.scales, n0, N, lane, tot);
 #pragma unroll
     for (int r = 0; r < kGemvRW; r++) {
       const int n = n0 + r;
@@ -243,28 +316,36 @@ __global__ __launch_bounds__(256) void qkv_proj_kernel(LayerView L, QkvProjArgs 
   if (lane == 0) __hip_atomic_store(&a.count[head], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int D, bool XLDS>
-static void launch_qkv_proj_d(const LayerView& L, const QkvProjArgs& a, dim3 g, size_t lds, hipStream_t st) {
-  switch (L.dtype) {
-    case KV_F32: hipLaunchKernelGGL((qkv_proj_kernel<D, KV_F32, XLDS>), g, dim3(256), lds, st, L, a); break;
-    case KV_F16: hipLaunchKernelGGL((qkv_proj_kernel<D, KV_F16, XLDS>), g, dim3(256), lds, st, L, a); break;
-    default: hipLaunchKernelGGL((qkv_proj_kernel<D, KV_Q8, XLDS>), g, dim3(256), lds, st, L, a); break;
+template <int D, int DT, int XM>
+static hipError_t launch_qkv_proj_k(const LayerView& L, const QkvProjArgs& a, dim3 g, size_t lds, hipStream_t st) {
+  if constexpr (XM == kXLut) {
+    const hipError_t e = gemv_allow_lds((const void*)qkv_proj_kernel<D, DT, XM>, lds);
+    if (e != hipSuccess) return e;
   }
+  hipLaunchKernelGGL((qkv_proj_kernel<D, DT, XM>), g, dim3(256), lds, st, L, a);
+  return hipGetLastError();
+}
+
+template <int D, int XM>
+static hipError_t launch_qkv_proj_d(const LayerView& L, const QkvProjArgs& a, dim3 g, size_t lds, hipStream_t st) {
+  switch (L.dtype) {
+    case KV_F32: return launch_qkv_proj_k<D, KV_F32, XM>(L, a, g, lds, st);
+    case KV_F16: return launch_qkv_proj_k<D, KV_F16, XM>(L, a, g, lds, st);
+    default: return launch_qkv_proj_k<D, KV_Q8, XM>(L, a, g, lds, st);
+  }
+}
+
+template <int D>
+static hipError_t launch_qkv_proj_x(const LayerView& L, const QkvProjArgs& a, dim3 g, hipStream_t st) {
+  if (a.K <= kLutMaxK) return launch_qkv_proj_d<D, kXLut>(L, a, g, gemv_lut_bytes(a.K), st);
+  if (a.K <= kGemvLdsMaxK) return launch_qkv_proj_d<D, kXLds>(L, a, g, (size_t)(a.K / 32) * kXPad * sizeof(float), st);
+  return launch_qkv_proj_d<D, kXGlobal>(L, a, g, 0, st);
 }
 
 hipError_t launch_qkv_proj(const LayerView& L, const QkvProjArgs& a, hipStream_t st) {
   const int N = (a.H + 2 * L.kv_heads) * L.D;
   const dim3 g(N / kQkvRowsPerWg);
-  const bool xlds = a.K <= kGemvLdsMaxK;
-  const size_t lds = xlds ? (size_t)(a.K / 32) * kXPad * sizeof(float) : 0;
-  if (L.D == 128) {
-    if (xlds) launch_qkv_proj_d<128, true>(L, a, g, lds, st);
-    else launch_qkv_proj_d<128, false>(L, a, g, lds, st);
-  } else {
-    if (xlds) launch_qkv_proj_d<256, true>(L, a, g, lds, st);
-    else launch_qkv_proj_d<256, false>(L, a, g, lds, st);
-  }
-  return hipGetLastError();
+  return L.D == 128 ? launch_qkv_proj_x<128>(L, a, g, st) : launch_qkv_proj_x<256>(L, a, g, st);
 }
 
 }  // namespace bg

@@ -51,9 +51,11 @@ def test_gemv_split_matches_oracle(dev, K, N0, N1, N2):
     _check_gemv(got, x, sign, sc)
 
 
-@pytest.mark.parametrize("K,N", [(4096, 4096), (12288, 4096), (4096, 2560), (384, 77)])
+@pytest.mark.parametrize("K,N", [(4096, 4096), (12288, 4096), (4096, 2560), (384, 77), (128, 64), (4224, 300), (12416, 200)])
 def test_gemv_resid_matches_oracle(dev, K, N):
-    """o_proj / down_proj with the residual (src/engine.ts:1547, matmul_resid_mr_sg.wgsl)."""
+    """o_proj / down_proj with the residual (src/engine.ts:1547, matmul_resid_mr_sg.wgsl): rows
+    read through the nibble table (K <= 4096, down to a single scale block), through x staged in
+    LDS (4224 just past the table, 12288) and from memory (12416, past the staging)."""
     rng = np.random.default_rng(K * 3 + N)
     sign, sc = _weight(rng, N, K)
     x = rng.standard_normal(K).astype(np.float32)
