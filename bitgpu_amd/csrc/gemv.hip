@@ -59,7 +59,47 @@ __host__ __device__ constexpr size_t gemv_lut_bytes(int K) { return (size_t)K * 
 // The nibble table: lut[(16 g + e) W + w] = sum over k < 4 of (bit k of e set ? +x : -x) of
 // x[32 w + 4 g + k], summed as (k0, k1) + (k2, k3): every signed combination of a nibble's four
 // x values (bit set = weight +1, as in the word loop). W-fastest, so the lanes' reads (one word
-// each) fall on distinct banks. The whole workgroup builds it, then a barrier.
+// each) fall on distinct banks. The 256 threads of the workgroup build it (at most 4 (word,
+// nibble) pairs each at K <= kLutMaxK) in two parts: in the GEMV the x loads are issued before
+// the weight loads (vector-memory waits retire in issue order, so the build then waits for x alone
+// and runs under the weights' latency), the table is written after them, then a barrier.
+constexpr int kLutPairsPerThread = 8 * (kLutMaxK / 32) / 256;
+struct LutX {
+  float4 v[kLutPairsPerThread];
+};
+// pair i = g W + w (i < 8 W <= 1024): g = floor(i * ceil(2^20 / W) / 2^20), exact for W < 1000
+__device__ __forceinline__ int lut_pair_g(int i, unsigned inv_w) { return (int)(__umul24((unsigned)i, inv_w) >> 20); }
+__device__ __forceinline__ void gemv_lut_load(const float* __restrict__ x, int K, LutX& X) {
+  const int W = K >> 5;
+  const unsigned inv_w = ((1u << 20) + W - 1) / W;
+#pragma unroll
+  for (int j = 0; j < kLutPairsPerThread; j++) {
+    const int i = threadIdx.x + 256 * j;
+    const int ic = i < 8 * W ? i : 8 * W - 1;  // unconditional load, as for the weights
+    const int g = lut_pair_g(ic, inv_w), w = ic - g * W;
+    X.v[j] = *(const float4*)(x + 32 * w + 4 * g);
+  }
+}
+__device__ __forceinline__ void gemv_lut_write(const LutX& X, float* lut, int K) {
+  const int W = K >> 5;
+  const unsigned inv_w = ((1u << 20) + W - 1) / W;
+#pragma unroll
+  for (int j = 0; j < kLutPairsPerThread; j++) {
+    const int i = threadIdx.x + 256 * j;
+    if (i < 8 * W) {
+      const int g = lut_pair_g(i, inv_w), w = i - g * W;
+      const float4 v = X.v[j];
+      const float a[4] = {-v.x - v.y, v.x - v.y, v.y - v.x, v.x + v.y};
+      const float b[4] = {-v.z - v.w, v.z - v.w, v.w - v.z, v.z + v.w};
+      float* d = lut + (size_t)(16 * g) * W + w;
+#pragma unroll
+      for (int e = 0; e < 16; e++) d[(size_t)e * W] = a[e & 3] + b[e >> 2];
+    }
+  }
+  __syncthreads();
+}
+// the fused qkv kernel builds its table in one loop after its weight loads (measured faster there
+// than the two-part order)
 __device__ __forceinline__ void gemv_build_lut(const float* __restrict__ x, float* lut, int K) {
   const int W = K >> 5;
   for (int i = threadIdx.x; i < 8 * W; i += blockDim.x) {
@@ -74,17 +114,30 @@ __device__ __forceinline__ void gemv_build_lut(const float* __restrict__ x, floa
   __syncthreads();
 }
 
-template <int RW>
+// BF: every load unconditional (clamped address, the value zeroed after), so no branch: the wait
+// counts stay exact and a later wait for loads issued before these does not drain them (the
+// GEMV's table build then waits for its x loads alone); otherwise rows past the end are not
+// loaded (measured faster for the fused qkv kernel, which builds its table after these loads)
+template <int RW, bool BF = false>
 __device__ __forceinline__ void gemv_load_w(GemvTile<RW>& T, int W, int NB, const uint32_t* __restrict__ sign,
                                             const float* __restrict__ scales, int n0, int n_rows, int t, int lane) {
   const int w = 64 * t + lane;
   const bool ok = w < W;
+  const int wc = ok ? w : W - 1;
 #pragma unroll
   for (int r = 0; r < RW; r++) {
     const int n = n0 + r;
     const bool v = ok && n < n_rows;
-    T.word[r] = v ? sign[(size_t)n * W + w] : 0u;
-    T.sc[r] = v ? scales[(size_t)n * NB + (w >> 2)] : 0.0f;
+    if constexpr (BF) {
+      const int nc = n < n_rows ? n : n_rows - 1;
+      const uint32_t wd = sign[(size_t)nc * W + wc];
+      const float sc = scales[(size_t)nc * NB + (wc >> 2)];
+      T.word[r] = v ? wd : 0u;
+      T.sc[r] = v ? sc : 0.0f;
+    } else {
+      T.word[r] = v ? sign[(size_t)n * W + w] : 0u;
+      T.sc[r] = v ? scales[(size_t)n * NB + (w >> 2)] : 0.0f;
+    }
   }
 }
 
@@ -106,11 +159,11 @@ __device__ __forceinline__ void gemv_load_x(GemvTile<RW>& T, const float* __rest
   }
 }
 
-template <int RW, int XM>
+template <int RW, int XM, bool BF>
 __device__ __forceinline__ void gemv_load(GemvTile<RW>& T, const float* __restrict__ x, const float* xs, int W, int NB,
                                           const uint32_t* __restrict__ sign, const float* __restrict__ scales,
                                           int n0, int n_rows, int t, int lane) {
-  gemv_load_w<RW>(T, W, NB, sign, scales, n0, n_rows, t, lane);
+  gemv_load_w<RW, BF>(T, W, NB, sign, scales, n0, n_rows, t, lane);
   gemv_load_x<RW, XM>(T, x, xs, W, t, lane);
 }
 
@@ -160,7 +213,7 @@ __device__ __forceinline__ void gemv_accumulate(const GemvTile<RW>& T, float (&a
 // (a uniform trip count, so the compiler keeps them outstanding across the loop head).
 // (the caller issues tile 0's weight loads into A, then stages x or builds the table, then calls
 // this; xs is the staged x or the table)
-template <int RW, int XM>
+template <int RW, int XM, bool BF>
 __device__ inline void gemv_rows(GemvTile<RW>& A, const float* __restrict__ x, const float* xs, int K,
                                  const uint32_t* __restrict__ sign, const float* __restrict__ scales, int n0, int n_rows,
                                  int lane, float (&tot)[RW]) {
@@ -173,9 +226,9 @@ __device__ inline void gemv_rows(GemvTile<RW>& A, const float* __restrict__ x, c
   gemv_load_x<RW, XM>(A, x, xs, W, 0, lane);
   int t = 0;
   for (; t + 2 <= n_tiles; t += 2) {
-    gemv_load<RW, XM>(B, x, xs, W, NB, sign, scales, n0, n_rows, t + 1, lane);
+    gemv_load<RW, XM, BF>(B, x, xs, W, NB, sign, scales, n0, n_rows, t + 1, lane);
     gemv_accumulate<RW, XM>(A, acc, xs, W, t, lane);
-    if (t + 2 < n_tiles) gemv_load<RW, XM>(A, x, xs, W, NB, sign, scales, n0, n_rows, t + 2, lane);
+    if (t + 2 < n_tiles) gemv_load<RW, XM, BF>(A, x, xs, W, NB, sign, scales, n0, n_rows, t + 2, lane);
     gemv_accumulate<RW, XM>(B, acc, xs, W, t + 1, lane);
   }
   if (t < n_tiles) gemv_accumulate<RW, XM>(A, acc, xs, W, t, lane);
@@ -191,14 +244,16 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   const int n0 = (blockIdx.x * 4 + wave) * kGemvRW;
   // lane r < kGemvRW stores row n0 + r: its residual and the first tile's weights are loaded
   // before x is staged
+  LutX X;
+  if constexpr (XM == kXLut) gemv_lut_load(a.x, a.K, X);
   const float res = (a.resid && lane < kGemvRW && n0 + lane < N) ? a.resid[n0 + lane] : 0.0f;
   GemvTile<kGemvRW> A;
-  gemv_load_w<kGemvRW>(A, a.K >> 5, a.K >> 7, a.sign, a.scales, n0, N, 0, lane);
+  gemv_load_w<kGemvRW, XM == kXLut>(A, a.K >> 5, a.K >> 7, a.sign, a.scales, n0, N, 0, lane);
   if constexpr (XM == kXLds) gemv_stage_x(a.x, xs, a.K);
-  if constexpr (XM == kXLut) gemv_build_lut(a.x, xs, a.K);
+  if constexpr (XM == kXLut) gemv_lut_write(X, xs, a.K);
   if (n0 >= N) return;  // wave-uniform
   float tot[kGemvRW];
-  gemv_rows<kGemvRW, XM>(A, a.x, xs, a.K, a.sign, a.scales, n0, N, lane, tot);
+  gemv_rows<kGemvRW, XM, XM == kXLut>(A, a.x, xs, a.K, a.sign, a.scales, n0, N, lane, tot);
 #pragma unroll
   for (int r = 0; r < kGemvRW; r++) {
     const int n = n0 + r;
@@ -265,7 +320,7 @@ __global__ __launch_bounds__(256) void qkv_proj_kernel(LayerView L, QkvProjArgs 
     if constexpr (XM == kXLds) gemv_stage_x(a.x, xs, a.K);
     if constexpr (XM == kXLut) gemv_build_lut(a.x, xs, a.K);
     float tot[kGemvRW];
-    gemv_rows<kGemvRW, XM>(A, a.x, xs, a.K, a.sign, a.scales, n0, N, lane, tot);
+    gemv_rows<kGemvRW, XM, false>(A, a.x, xs, a.K, a.sign, a.scales, n0, N, lane, tot);
 #pragma unroll
     for (int r = 0; r < kGemvRW; r++) {
       const int n = n0 + r;
