@@ -300,7 +300,7 @@ __global__ __launch_bounds__(256) void attn_f32_split_kernel(LayerView L, AttnAr
   wait_stores();
   __syncthreads();
   if (tid == 0) {
-    const unsigned prev = __hip_atomic_fetch_add(&a.ws_count[kvh], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned prev = __hip_atomic_fetch_add(&a.ws_count[kvh * kCounterStride], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = prev == (unsigned)(sp.n_splits - 1) ? 1u : 0u;
   }
   __syncthreads();
@@ -325,7 +325,7 @@ __global__ __launch_bounds__(256) void attn_f32_split_kernel(LayerView L, AttnAr
     a.out[((size_t)s * a.H + h) * D + d] = res;
   }
   __syncthreads();
-  if (tid == 0) __hip_atomic_store(&a.ws_count[kvh], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (tid == 0) __hip_atomic_store(&a.ws_count[kvh * kCounterStride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 bool f32_split_supported(const LayerView& L, int S, int H) {

@@ -399,8 +399,8 @@ int32_t bg_kv_create(int32_t n_layers, int32_t kv_heads, int32_t head_dim, int32
   hipError_t e = hipHostMalloc((void**)&c->err_host, 64, hipHostMallocMapped | hipHostMallocCoherent);
   if (e == hipSuccess) e = hipHostGetDevicePointer((void**)&c->err_dev, c->err_host, 0);
   if (e == hipSuccess) e = hipMalloc((void**)&c->proj_raw, (size_t)2 * kv_heads * head_dim * sizeof(float));
-  if (e == hipSuccess) e = hipMalloc((void**)&c->proj_count, (size_t)kProjMaxHeads * bg::kProjCountStride * sizeof(unsigned));
-  if (e == hipSuccess) e = hipMemset(c->proj_count, 0, (size_t)kProjMaxHeads * bg::kProjCountStride * sizeof(unsigned));
+  if (e == hipSuccess) e = hipMalloc((void**)&c->proj_count, (size_t)kProjMaxHeads * bg::kCounterStride * sizeof(unsigned));
+  if (e == hipSuccess) e = hipMemset(c->proj_count, 0, (size_t)kProjMaxHeads * bg::kCounterStride * sizeof(unsigned));
   if (e != hipSuccess) {
     if (c->err_host) (void)hipHostFree(c->err_host);
     if (c->proj_raw) (void)hipFree(c->proj_raw);

@@ -72,11 +72,12 @@ struct QkvProjArgs {
   int pos, slot;
   float* q_out;                    // [H, D]: raw rows first, then the normed, roped rows
   float* kv_raw;                   // [2 KV D] raw K and V rows
-  unsigned* count;                 // [H + 2 KV] arrival counters kProjCountStride apart, zero between launches
+  unsigned* count;                 // [H + 2 KV] arrival counters kCounterStride apart, zero between launches
 };
-// Arrival counters sit 256 bytes apart: 384 workgroups' atomics on counters packed into two
-// lines serialize (the 8B-shape qkv projection took 8.6 us with them packed, 7.5 us apart).
-constexpr int kProjCountStride = 64;
+// Arrival counters (the fused projection's per head, the f32 decode's per kv head) sit 256 bytes
+// apart: 384 workgroups' atomics on counters packed into two lines serialize (the 8B-shape qkv
+// projection took 8.6 us with them packed, 7.5 us apart).
+constexpr int kCounterStride = 64;
 hipError_t launch_qkv_proj(const LayerView& L, const QkvProjArgs& a, hipStream_t st);
 
 // attention (decode.hip, attn_f32.hip, prefill.hip)

@@ -1054,7 +1054,7 @@ size_t decode_workspace_floats(const LayerView& L, int S, int H, int num_cus, si
   const int R = (H / L.kv_heads) * S;
   int ns_max = (L.cap / 32 + 3) / 4;
   ns_max = ns_max < kMaxSplits ? ns_max : kMaxSplits;
-  *counters = (size_t)L.kv_heads;
+  *counters = (size_t)L.kv_heads * kCounterStride;
   return (size_t)L.kv_heads * R * (L.D / 64) * ns_max * kUnitF4 * 4;
 }
 

@@ -340,7 +340,7 @@ __global__ __launch_bounds__(256) void qkv_proj_kernel(LayerView L, QkvProjArgs 
   wait_stores();
   __syncthreads();
   if (threadIdx.x == 0) {
-    const unsigned prev = __hip_atomic_fetch_add(&a.count[head * kProjCountStride], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned prev = __hip_atomic_fetch_add(&a.count[head * kCounterStride], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = prev == (unsigned)(D / kQkvRowsPerWg - 1) ? 1u : 0u;
   }
   __syncthreads();
@@ -378,7 +378,7 @@ __global__ __launch_bounds__(256) void qkv_proj_kernel(LayerView L, QkvProjArgs 
   } else {
     if (D == 256 || writer) store_v4<D, DT>(L, L.ring.phys(a.slot), head - a.H - KV, x, c);
   }
-  if (lane == 0) __hip_atomic_store(&a.count[head * kProjCountStride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (lane == 0) __hip_atomic_store(&a.count[head * kCounterStride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int D, int DT, int XM>
