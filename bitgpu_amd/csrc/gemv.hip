@@ -20,7 +20,7 @@
 //           times the word's block scale; a DPP / permlane wave sum finishes the row. Two tiles'
 //           loads (the rows' words and scales, x) are in flight: the next tile is issued before
 //           the current one's arithmetic; the residual is loaded at the start.
-//   fused   the qkv kernel's workgroups own 16 rows of one head; each stores its raw rows (Q
+//   fused   the qkv kernel's workgroups own 32 rows of one head; each stores its raw rows (Q
 //           into q_out, K and V into the cache's small raw buffer), and the last workgroup of a
 //           head to arrive (an arrival counter per head, 256 bytes apart, reset by that
 //           workgroup; a head's workgroups placed on one XCD) normalizes
@@ -300,10 +300,13 @@ hipError_t launch_gemv(const GemvArgs& a, hipStream_t st) {
 }
 
 // ---- fused decode qkv projection + prologue ---------------------------------------------------
-constexpr int kQkvRowsPerWg = 4 * kGemvRW;  // 16 rows of one head
+// 32 rows of one head a workgroup of 8 waves: the 8B shape's 192 workgroups one a CU (6.7 us)
+// against 384 of 16 rows, two on half the CUs (7.3 us), or 96 of 64 rows (7.5 us)
+constexpr int kQkvRowsPerWg = 8 * kGemvRW;
+constexpr int kQkvThreads = 64 * kQkvRowsPerWg / kGemvRW;
 
 template <int D, int DT, int XM>
-__global__ __launch_bounds__(256) void qkv_proj_kernel(LayerView L, QkvProjArgs a) {
+__global__ __launch_bounds__(kQkvThreads) void qkv_proj_kernel(LayerView L, QkvProjArgs a) {
   constexpr int LPR = D / 4;  // lanes per row in the epilogue
   extern __shared__ __align__(16) float xs[];
   __shared__ __align__(16) float rrow[D];
@@ -387,7 +390,7 @@ static hipError_t launch_qkv_proj_k(const LayerView& L, const QkvProjArgs& a, di
     const hipError_t e = gemv_allow_lds((const void*)qkv_proj_kernel<D, DT, XM>, lds);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL((qkv_proj_kernel<D, DT, XM>), g, dim3(256), lds, st, L, a);
+  hipLaunchKernelGGL((qkv_proj_kernel<D, DT, XM>), g, dim3(kQkvThreads), lds, st, L, a);
   return hipGetLastError();
 }
 
