@@ -34,7 +34,12 @@
 
 namespace bg {
 
-constexpr int kGemvRW = 4;  // rows per wave
+// 2 rows a wave, 8 waves a workgroup (16 rows): o_proj at the 8B shape 3.8 us against 4.4 with 4
+// rows on 4 waves (the same rows a workgroup, twice the waves to cover the loads' latency), 4.3
+// with 4 rows on 8 waves
+constexpr int kGemvRW = 2;
+constexpr int kGemvWaves = 8;
+constexpr int kGemvThreads = 64 * kGemvWaves;
 
 // One 2048-weight tile of a wave's rows: the lane's sign word (word 64t + l) and block scale of
 // each row and the 32 x values under the word.
@@ -60,11 +65,11 @@ __host__ __device__ constexpr size_t gemv_lut_bytes(int K) { return (size_t)K * 
 // The nibble table: lut[(16 g + e) W + w] = sum over k < 4 of (bit k of e set ? +x : -x) of
 // x[32 w + 4 g + k], summed as (k0, k1) + (k2, k3): every signed combination of a nibble's four
 // x values (bit set = weight +1, as in the word loop). W-fastest, so the lanes' reads (one word
-// each) fall on distinct banks. The 256 threads of the workgroup build it (at most 4 (word,
+// each) fall on distinct banks. The kGemvThreads threads of the workgroup build it (at most 2 (word,
 // nibble) pairs each at K <= kLutMaxK) in two parts: in the GEMV the x loads are issued before
 // the weight loads (vector-memory waits retire in issue order, so the build then waits for x alone
 // and runs under the weights' latency), the table is written after them, then a barrier.
-constexpr int kLutPairsPerThread = 8 * (kLutMaxK / 32) / 256;
+constexpr int kLutPairsPerThread = 8 * (kLutMaxK / 32) / kGemvThreads;
 struct LutX {
   float4 v[kLutPairsPerThread];
 };
@@ -75,7 +80,7 @@ __device__ __forceinline__ void gemv_lut_load(const float* __restrict__ x, int K
   const unsigned inv_w = ((1u << 20) + W - 1) / W;
 #pragma unroll
   for (int j = 0; j < kLutPairsPerThread; j++) {
-    const int i = threadIdx.x + 256 * j;
+    const int i = threadIdx.x + kGemvThreads * j;
     const int ic = i < 8 * W ? i : 8 * W - 1;  // unconditional load, as for the weights
     const int g = lut_pair_g(ic, inv_w), w = ic - g * W;
     X.v[j] = *(const float4*)(x + 32 * w + 4 * g);
@@ -86,7 +91,7 @@ __device__ __forceinline__ void gemv_lut_write(const LutX& X, float* lut, int K)
   const unsigned inv_w = ((1u << 20) + W - 1) / W;
 #pragma unroll
   for (int j = 0; j < kLutPairsPerThread; j++) {
-    const int i = threadIdx.x + 256 * j;
+    const int i = threadIdx.x + kGemvThreads * j;
     if (i < 8 * W) {
       const int g = lut_pair_g(i, inv_w), w = i - g * W;
       const float4 v = X.v[j];
@@ -238,11 +243,11 @@ __device__ inline void gemv_rows(GemvTile<RW>& A, const float* __restrict__ x, c
 }
 
 template <int XM>
-__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
+__global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
   extern __shared__ __align__(16) float xs[];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int N = a.N0 + a.N1 + a.N2;
-  const int n0 = (blockIdx.x * 4 + wave) * kGemvRW;
+  const int n0 = (blockIdx.x * kGemvWaves + wave) * kGemvRW;
   // lane r < kGemvRW stores row n0 + r: its residual and the first tile's weights are loaded
   // before x is staged
   LutX X;
@@ -284,25 +289,25 @@ hipError_t launch_gemv(const GemvArgs& a, hipStream_t st) {
   const int N = a.N0 + a.N1 + a.N2;
   if (N <= 0) return hipSuccess;
   const int waves = (N + kGemvRW - 1) / kGemvRW;
-  const dim3 g((waves + 3) / 4);
+  const dim3 g((waves + kGemvWaves - 1) / kGemvWaves);
   if (a.K <= kLutMaxK) {
     const size_t lds = gemv_lut_bytes(a.K);
     const hipError_t e = gemv_allow_lds((const void*)gemv_kernel<kXLut>, lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(gemv_kernel<kXLut>, g, dim3(256), lds, st, a);
+    hipLaunchKernelGGL(gemv_kernel<kXLut>, g, dim3(kGemvThreads), lds, st, a);
   } else if (a.K <= kGemvLdsMaxK) {
     const size_t lds = (size_t)(a.K / 32) * kXPad * sizeof(float);
-    hipLaunchKernelGGL(gemv_kernel<kXLds>, g, dim3(256), lds, st, a);
+    hipLaunchKernelGGL(gemv_kernel<kXLds>, g, dim3(kGemvThreads), lds, st, a);
   } else {
-    hipLaunchKernelGGL(gemv_kernel<kXGlobal>, g, dim3(256), 0, st, a);
+    hipLaunchKernelGGL(gemv_kernel<kXGlobal>, g, dim3(kGemvThreads), 0, st, a);
   }
   return hipGetLastError();
 }
 
 // ---- fused decode qkv projection + prologue ---------------------------------------------------
-// 32 rows of one head a workgroup of 8 waves: the 8B shape's 192 workgroups one a CU (6.7 us)
-// against 384 of 16 rows, two on half the CUs (7.3 us), or 96 of 64 rows (7.5 us)
-constexpr int kQkvRowsPerWg = 8 * kGemvRW;
+// 32 rows of one head a workgroup (16 waves of kGemvRW rows): the 8B shape's 192 workgroups one
+// a CU, 6.7 us against 384 of 16 rows, two on half the CUs (7.3 us), or 96 of 64 rows (7.5 us)
+constexpr int kQkvRowsPerWg = 32;
 constexpr int kQkvThreads = 64 * kQkvRowsPerWg / kGemvRW;
 
 template <int D, int DT, int XM>
