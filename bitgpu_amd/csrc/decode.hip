@@ -787,7 +787,11 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
   // Thread (k, c) holds float4 column c of splits k, k + KG, .. (MAXL at a time); wave 0 also
   // holds (m, l) of every split, one per lane.
   constexpr int KG = NTHR / 16;                // split groups
-  constexpr int MAXL = 4;                      // o slots per thread and batch
+  // o slots per thread and batch (KG * MAXL splits a batch: 64 on 4 waves); 5 for the D=256
+  // one-tile kernel (4 waves, 80 a batch), whose 8193-8448-slot contexts (257-264 tiles) take
+  // 65-66 splits a kv head: one poll round instead of two (C5 decode 17.6 -> 16.95 us; 5 slots
+  // cost the D=128 one-tile kernel 0.1 us at 4k)
+  constexpr int MAXL = (ONE && D == 256) ? 5 : 4;
   constexpr int MLC = (kMaxSplits + 63) / 64;  // (m, l) slots per lane of wave 0
   const int c = tid & 15, k = tid >> 4;
   float* wts = (float*)smem;                                   // [NS]
