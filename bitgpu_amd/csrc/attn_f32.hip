@@ -119,6 +119,9 @@ struct F32Split {
   float qscale;  // scale * log2(e)
 };
 
+// splits a merge reads in one batch (same order and arithmetic as the loop past it)
+constexpr int kF32MergeBatch = 16;
+
 template <int D, bool ROLL, int RM>
 __global__ __launch_bounds__(256) void attn_f32_split_kernel(LayerView L, AttnArgs a, F32Split sp) {
   constexpr int EPL = D / 64;   // output dims per lane
@@ -311,13 +314,36 @@ __global__ __launch_bounds__(256) void attn_f32_split_kernel(LayerView L, AttnAr
   for (int i = tid; i < R * D; i += 256) {
     const int r = i / D, d = i % D;
     float M = -1e30f;
-    for (int q = 0; q < NS; q++) M = fmaxf(M, ld_coherent2(&wml[((size_t)q * R + r) * 2]).x);
     float o = 0.0f, lt = 0.0f;
-    for (int q = 0; q < NS; q++) {
-      const float2 ml = ld_coherent2(&wml[((size_t)q * R + r) * 2]);
-      const float f = exp2f(ml.x - M);
-      o += ld_coherent(&wo[(size_t)q * R * D + i]) * f;
-      lt += ml.y * f;
+    if (NS <= kF32MergeBatch) {
+      // every split's (m, l) and o issued before any is used: one memory round trip instead of
+      // one per split (the loop below waits for each load; C1 9.2 -> 7.3 us per layer)
+      float2 mlv[kF32MergeBatch];
+      float ov[kF32MergeBatch];
+#pragma unroll
+      for (int q = 0; q < kF32MergeBatch; q++) {
+        const int qc = q < NS ? q : NS - 1;
+        mlv[q] = ld_coherent2(&wml[((size_t)qc * R + r) * 2]);
+        ov[q] = ld_coherent(&wo[(size_t)qc * R * D + i]);
+      }
+#pragma unroll
+      for (int q = 0; q < kF32MergeBatch; q++) M = q < NS ? fmaxf(M, mlv[q].x) : M;
+#pragma unroll
+      for (int q = 0; q < kF32MergeBatch; q++) {
+        if (q < NS) {
+          const float f = exp2f(mlv[q].x - M);
+          o += ov[q] * f;
+          lt += mlv[q].y * f;
+        }
+      }
+    } else {
+      for (int q = 0; q < NS; q++) M = fmaxf(M, ld_coherent2(&wml[((size_t)q * R + r) * 2]).x);
+      for (int q = 0; q < NS; q++) {
+        const float2 ml = ld_coherent2(&wml[((size_t)q * R + r) * 2]);
+        const float f = exp2f(ml.x - M);
+        o += ld_coherent(&wo[(size_t)q * R * D + i]) * f;
+        lt += ml.y * f;
+      }
     }
     const int s = r / sp.G, h = kvh * sp.G + r % sp.G;
     float res = o / lt;
