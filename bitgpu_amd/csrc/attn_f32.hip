@@ -122,7 +122,8 @@ struct F32Split {
 // splits a merge reads in one batch (same order and arithmetic as the loop past it)
 constexpr int kF32MergeBatch = 16;
 
-template <int D, bool ROLL, int RM>
+// MB: more than kF32MergeBatch splits (a separate instantiation, so the short merge keeps its code)
+template <int D, bool ROLL, int RM, bool MB>
 __global__ __launch_bounds__(256) void attn_f32_split_kernel(LayerView L, AttnArgs a, F32Split sp) {
   constexpr int EPL = D / 64;   // output dims per lane
   constexpr int DQ = D / 4;     // K dims per lane group
@@ -315,9 +316,9 @@ __global__ __launch_bounds__(256) void attn_f32_split_kernel(LayerView L, AttnAr
     const int r = i / D, d = i % D;
     float M = -1e30f;
     float o = 0.0f, lt = 0.0f;
-    if (NS <= kF32MergeBatch) {
+    if constexpr (!MB) {
       // every split's (m, l) and o issued before any is used: one memory round trip instead of
-      // one per split (the loop below waits for each load; C1 9.2 -> 7.3 us per layer)
+      // one per split (a loop that waits for each load: C1 9.2 against 7.3 us per layer)
       float2 mlv[kF32MergeBatch];
       float ov[kF32MergeBatch];
 #pragma unroll
@@ -337,12 +338,35 @@ __global__ __launch_bounds__(256) void attn_f32_split_kernel(LayerView L, AttnAr
         }
       }
     } else {
-      for (int q = 0; q < NS; q++) M = fmaxf(M, ld_coherent2(&wml[((size_t)q * R + r) * 2]).x);
-      for (int q = 0; q < NS; q++) {
-        const float2 ml = ld_coherent2(&wml[((size_t)q * R + r) * 2]);
-        const float f = exp2f(ml.x - M);
-        o += ld_coherent(&wo[(size_t)q * R * D + i]) * f;
-        lt += ml.y * f;
+      // more splits: the same in batches of kF32MergeBatch, a pass for the maximum, then one for
+      // the sums (split order kept)
+      for (int q0 = 0; q0 < NS; q0 += kF32MergeBatch) {
+        float mv[kF32MergeBatch];
+#pragma unroll
+        for (int j = 0; j < kF32MergeBatch; j++) {
+          const int qc = q0 + j < NS ? q0 + j : NS - 1;
+          mv[j] = ld_coherent2(&wml[((size_t)qc * R + r) * 2]).x;
+        }
+#pragma unroll
+        for (int j = 0; j < kF32MergeBatch; j++) M = q0 + j < NS ? fmaxf(M, mv[j]) : M;
+      }
+      for (int q0 = 0; q0 < NS; q0 += kF32MergeBatch) {
+        float2 mlv[kF32MergeBatch];
+        float ov[kF32MergeBatch];
+#pragma unroll
+        for (int j = 0; j < kF32MergeBatch; j++) {
+          const int qc = q0 + j < NS ? q0 + j : NS - 1;
+          mlv[j] = ld_coherent2(&wml[((size_t)qc * R + r) * 2]);
+          ov[j] = ld_coherent(&wo[(size_t)qc * R * D + i]);
+        }
+#pragma unroll
+        for (int j = 0; j < kF32MergeBatch; j++) {
+          if (q0 + j < NS) {
+            const float f = exp2f(mlv[j].x - M);
+            o += ov[j] * f;
+            lt += mlv[j].y * f;
+          }
+        }
       }
     }
     const int s = r / sp.G, h = kvh * sp.G + r % sp.G;
@@ -369,7 +393,12 @@ size_t f32_workspace_floats(const LayerView& L, int S, int H) {
 
 template <int D, bool ROLL, int RM>
 static void launch_split_rm(const LayerView& L, const AttnArgs& a, const F32Split& sp, hipStream_t st) {
-  hipLaunchKernelGGL((attn_f32_split_kernel<D, ROLL, RM>), dim3(sp.n_splits * L.kv_heads), dim3(256), 0, st, L, a, sp);
+  // splits beyond one merge batch (long f32 contexts): 1500 / 4096 / 16384 slots 24.7 / 33.2 / 47.9
+  // -> 12.3 / 15.7 / 31.3 us with the batched passes
+  if (sp.n_splits > kF32MergeBatch)
+    hipLaunchKernelGGL((attn_f32_split_kernel<D, ROLL, RM, true>), dim3(sp.n_splits * L.kv_heads), dim3(256), 0, st, L, a, sp);
+  else
+    hipLaunchKernelGGL((attn_f32_split_kernel<D, ROLL, RM, false>), dim3(sp.n_splits * L.kv_heads), dim3(256), 0, st, L, a, sp);
 }
 
 template <int D, bool ROLL>
