@@ -178,7 +178,8 @@ def test_decode_workspace_reuse(dev, dtype):
 
 
 # ------------------------------------------------------------------ f32 kernel
-@pytest.mark.parametrize("S,L", [(1, 1), (1, 100), (7, 40), (64, 64)])
+# (1, 1500) and (3, 4100): the split kernel with 24 and 65 splits a kv head, past one merge batch
+@pytest.mark.parametrize("S,L", [(1, 1), (1, 100), (7, 40), (64, 64), (1, 1500), (3, 4100)])
 def test_f32_kernel(dev, S, L):
     out, exp = _raw_case("f32", 16, 4, 128, L, S, seed=S * 1000 + L)
     _check("f32", out, exp)
