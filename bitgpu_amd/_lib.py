@@ -35,6 +35,7 @@ SIGNATURES = [
     ("bg_stream_sync", _i32, [_vp]),
     ("bg_decode_plan", _i32, [_i32] * 8 + [_pi32]),
     ("bg_diag_stream_read", _i32, [_vp, C.c_size_t, _i32, _i32, _vp, _vp]),
+    ("bg_debug_merge_hooks", _i32, [_i32, _i32]),
     ("bg_stream_create", _i32, [C.POINTER(_vp)]),
     ("bg_stream_destroy", _i32, [_vp]),
     ("bg_event_create", _i32, [C.POINTER(_vp)]),

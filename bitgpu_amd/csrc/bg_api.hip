@@ -8,6 +8,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <atomic>
 #include <mutex>
 #include <set>
 #include <string>
@@ -45,6 +46,7 @@ struct bg_kv_cache {
   std::vector<unsigned*> retired_count;
   int pf16_cap = 0;
   int num_cus = 256;
+  int device = 0;
   int q8_row = 0;     // q8: one scale per row (bg_kv_set_q8_block with head_dim)
   // decode merge error word: pinned, coherent host memory the kernel writes when a merger's
   // bounded wait gives up (err_dev is its device address)
@@ -155,9 +157,35 @@ __global__ void fill_u32_kernel(uint32_t* p, uint32_t value, size_t n) {
 std::mutex g_caches_mu;
 std::set<bg_kv_cache*> g_caches;
 
-int env_int(const char* name, int dflt) {
-  const char* v = getenv(name);
-  return (v && *v) ? atoi(v) : dflt;
+// test hooks of the decode merge (bg_debug_merge_hooks): a poll bound and a split that stores
+// no partial; 0 and -1 in normal use
+std::atomic<int> g_merge_spin{0};
+std::atomic<int> g_withhold_split{-1};
+
+// Workgroup placement per device: > 0 the XCD count when workgroups go to XCDs round robin
+// (the decode kernel's L2 partial exchange is on), -1 probed and off (no round robin, or a
+// merger later found itself on another XCD than its splits), 0 not probed yet.
+std::mutex g_xcd_mu;
+int g_xcd_state[kMaxDevices] = {};
+
+int xcd_state(int dev) {
+  if (dev < 0 || dev >= kMaxDevices) return -1;
+  std::lock_guard<std::mutex> lock(g_xcd_mu);
+  if (g_xcd_state[dev] == 0) {
+    int nx = 0;
+    if (bg::probe_xcd_round_robin(&nx) != hipSuccess) {
+      (void)hipGetLastError();
+      nx = 0;
+    }
+    g_xcd_state[dev] = nx > 0 ? nx : -1;
+  }
+  return g_xcd_state[dev];
+}
+
+void xcd_disable(int dev) {
+  if (dev < 0 || dev >= kMaxDevices) return;
+  std::lock_guard<std::mutex> lock(g_xcd_mu);
+  g_xcd_state[dev] = -1;
 }
 
 bool capturing(hipStream_t st) {
@@ -173,7 +201,11 @@ bool capturing(hipStream_t st) {
 // stored as NaN): wait for every launch to finish, refill the split workspace with the empty
 // marker (a late partial may have landed after its merger gave up) and report it once.
 int32_t take_merge_error(bg_kv_cache* c, hipStream_t st) {
-  if (!c->err_host || __atomic_load_n(c->err_host, __ATOMIC_ACQUIRE) == 0) return BG_OK;
+  const unsigned code = c->err_host ? __atomic_load_n(c->err_host, __ATOMIC_ACQUIRE) : 0u;
+  if (code == 0) return BG_OK;
+  // 2: a merger ran on another XCD than the splits whose partials it waited for (the L2
+  // exchange relies on round-robin placement): use written-through partials from now on
+  if (code == 2) xcd_disable(c->device);
   if (capturing(st))
     return fail(BG_E_DEVICE, "an earlier decode split merge gave up waiting for a split; call bg_stream_sync "
                              "outside graph capture to reset the workspace");
@@ -192,9 +224,15 @@ int32_t take_merge_error(bg_kv_cache* c, hipStream_t st) {
   if (e == hipSuccess) e = hipDeviceSynchronize();
   if (e != hipSuccess) return hip_fail(e, "workspace reset after a merge timeout");
   __atomic_store_n(c->err_host, 0u, __ATOMIC_RELEASE);
-  return fail(BG_E_DEVICE, "decode split merge gave up waiting for a split (GPU shared or oversubscribed): the "
-                           "outputs of bg_attention calls on this cache since the last check are NaN; the split "
-                           "workspace has been reset");
+  if (code == 2)
+    return fail(BG_E_DEVICE, "decode split merge gave up waiting for a split: a merging workgroup ran on another "
+                             "XCD than its splits, so their partials stayed in that XCD's L2; partials are written "
+                             "through to memory from now on. Outputs of bg_attention calls on this cache since the last "
+                             "check may be wrong (the merge that gave up stored NaN); the split workspace has been reset");
+  return fail(BG_E_DEVICE, "decode split merge gave up waiting for a split (GPU shared or oversubscribed): outputs "
+                           "of bg_attention calls on this cache since the last check may be wrong (the merge that gave "
+                           "up stored NaN; a partial that landed after it can have been taken by a later launch); the "
+                           "split workspace has been reset");
 }
 
 }  // namespace
@@ -202,6 +240,13 @@ int32_t take_merge_error(bg_kv_cache* c, hipStream_t st) {
 extern "C" {
 
 const char* bg_last_error_message(void) { return g_err.c_str(); }
+
+int32_t bg_debug_merge_hooks(int32_t spin_limit, int32_t withhold_split) {
+  if (spin_limit < 0) return fail(BG_E_INVALID, "bg_debug_merge_hooks: spin_limit %d < 0", spin_limit);
+  g_merge_spin.store(spin_limit, std::memory_order_relaxed);
+  g_withhold_split.store(withhold_split < 0 ? -1 : withhold_split, std::memory_order_relaxed);
+  return BG_OK;
+}
 
 const char* bg_version(void) { return "bitgpu-mi355x-attn 0.1.0 (gfx950)"; }
 
@@ -371,8 +416,10 @@ int32_t bg_kv_create(int32_t n_layers, int32_t kv_heads, int32_t head_dim, int32
   c->cap = round32(c->capacity);
   int dev = 0;
   (void)hipGetDevice(&dev);
+  c->device = dev;
   int cus = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0) c->num_cus = cus;
+  (void)xcd_state(dev);  // probe the workgroup placement once per device
   const size_t row = (size_t)c->cap * kv_heads * head_dim * elem_bytes(dtype);
   const size_t srow = (size_t)c->cap * kv_heads * (head_dim / 32) * sizeof(float);
   for (int l = 0; l < n_layers; l++) {
@@ -720,11 +767,11 @@ static bg::AttnArgs attention_args(bg_kv_cache* c, const float* q, int32_t S, in
   a.ws_count = nullptr;
   a.ws_floats = 0;
   a.num_cus = c->num_cus;
-  // test hooks (host-set): a tiny poll bound and a split that stores no partial make the merge
-  // give up while every kernel still exits normally
   a.err = c->err_dev;
-  a.spin_limit = env_int("BG_DEBUG_MERGE_SPIN", 0);
-  a.withhold_split = env_int("BG_DEBUG_WITHHOLD_SPLIT", -1);
+  a.spin_limit = g_merge_spin.load(std::memory_order_relaxed);
+  a.withhold_split = g_withhold_split.load(std::memory_order_relaxed);
+  const int xs = xcd_state(c->device);
+  a.n_xcd = xs > 0 ? xs : 0;
   return a;
 }
 

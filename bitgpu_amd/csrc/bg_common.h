@@ -166,6 +166,13 @@ __device__ inline float2 ld_coherent2(const float* p) {
 }
 __device__ inline void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// the XCD (accelerator complex die) this wave runs on: hardware register XCC_ID, bits 3:0
+__device__ inline int xcc_id() {
+  unsigned x;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+  return (int)(x & 0xf);
+}
+
 // Streaming (nontemporal) vector stores of data no kernel re-reads soon from the cache hierarchy:
 // a device copy moves 6.2 TB/s read + write with them against 5.4 TB/s with plain stores.
 __device__ inline void st_stream16(void* p, uint32_t a, uint32_t b, uint32_t c, uint32_t d) {

@@ -97,7 +97,14 @@ struct AttnArgs {
   // decode merge: host-visible error word, poll bound (0: default) and a test hook that makes
   // one split store no partial (-1: none)
   unsigned* err; int spin_limit; int withhold_split;
+  // XCDs the GPU dispatches workgroups to round robin (workgroup b on XCD (b + r) mod n_xcd, r
+  // the same for the whole grid; checked on the device once): the decode kernel then exchanges
+  // split partials through one XCD's L2. 0: partials are written through to memory.
+  int n_xcd;
 };
+// workgroup placement check of the current device: n_xcd > 0 when a probe grid's workgroups all
+// ran on XCD (blockIdx + r) mod n_xcd for one r (decode.hip)
+hipError_t probe_xcd_round_robin(int* n_xcd);
 hipError_t launch_attention_f32(const LayerView& L, const AttnArgs& a, hipStream_t st);
 // split-K f32 decode / verify (G*S <= 16 rows per kv head), workspace as for the decode kernel
 hipError_t launch_attention_f32_split(const LayerView& L, const AttnArgs& a, hipStream_t st);

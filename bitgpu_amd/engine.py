@@ -234,17 +234,24 @@ class KvCache:
             snap["roll"] = {"sinkTokens": self.sinks, "cacheLen": length, "evicted": self.ring_state()[1]}
         return snap
 
-    def restore_cache(self, snap: dict, model: dict | None = None, cache_len: int = 0, history=()) -> int:
+    def restore_cache(self, snap: dict, model: dict | None = None, cache_len: int = 0, history=(),
+                      hybrid: bool = False) -> int:
         """restoreCache (src/engine.ts:2807-2872): validate ``snap`` against this cache (same
         rejections and messages as the reference), then write its positions. ``cache_len`` and
         ``history`` are the engine's current cacheLen / fullHistory (a delta restore must sit
-        exactly on its prefix). Returns the restored cacheLen. A v2 snapshot restores into the
-        compacted ring (origin 0), the reference's layout after any eviction."""
+        exactly on its prefix); ``hybrid`` marks the qwen3_5 hybrid backbone, which takes full
+        snapshots only. Returns the restored cacheLen. A v2 snapshot restores into the
+        compacted ring (origin 0), the reference's layout after any eviction.
+
+        As in the reference, nothing is written before every check has passed and the capacity
+        has grown (ensureKvCapacity, 2846): a failed growth leaves the ring state and contents
+        as they were."""
         length, base, count = validate_snapshot(
             snap, roll=self.roll, sinks=self.sinks, kv_cache=self.kv_cache,
             model=dict(model) if model else self.model_stamp(), max_seq_len=self.max_seq_len,
             data_bytes=self.n_layers * sum(self.region_bytes(r, 1) for r in self._regions()),
-            cache_len=cache_len, history=history)
+            cache_len=cache_len, history=history, hybrid=hybrid)
+        self.ensure_capacity(length)
         if self.roll:
             self.ring_reset(int(snap["roll"].get("evicted", 0)))
         self.restore_snapshot(snap["data"], length, base)
@@ -266,9 +273,10 @@ class KvCache:
 
 
 def validate_snapshot(snap, *, roll: bool, sinks: int, kv_cache: str, model: dict, max_seq_len: int,
-                      data_bytes: int, cache_len: int = 0, history=()):
+                      data_bytes: int, cache_len: int = 0, history=(), hybrid: bool = False):
     """The checks of restoreCache (src/engine.ts:2808-2845), host-only, in the reference's order
-    and wording. ``data_bytes`` is snapshotBytes(1) (per-position bytes over every layer).
+    and wording. ``data_bytes`` is snapshotBytes(1) (per-position bytes over every layer);
+    ``hybrid`` is the engine's A.hybrid (the qwen3_5 backbone rejects delta snapshots, 2828).
     Raises BitgpuError; returns (len, base, count)."""
     def bad(msg):
         raise BitgpuError(BG_E_INVALID, msg)
@@ -294,6 +302,8 @@ def validate_snapshot(snap, *, roll: bool, sinks: int, kv_cache: str, model: dic
         bad("restoreCache: snapshot holds no tokens")
     length = int(rollinfo["cacheLen"]) if v2 else len(ids) - 1
     base = max(0, int(math.floor(snap.get("base") or 0)))
+    if base > 0 and hybrid:
+        bad("restoreCache: delta snapshots are not supported for the qwen3_5 hybrid backbone")
     count = length - base
     need = length + (0 if v2 else 1)
     if need > max_seq_len:

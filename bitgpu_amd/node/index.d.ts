@@ -1,7 +1,10 @@
 // Types of the JS shim (index.js) for a TypeScript host. Device pointers and streams are bigint.
 export type DevPtr = bigint
 export declare const K: 0, V: 1, KSCALE: 2, VSCALE: 3
-export declare class GpuOutOfMemoryError extends Error { code?: number }
+// the reference's class (src/errors.ts:14-19): name 'GpuOutOfMemoryError'; a host passes its own
+// class to setErrorClasses so that its instanceof checks match what the shim throws
+export declare class GpuOutOfMemoryError extends Error { readonly name: 'GpuOutOfMemoryError'; code?: number }
+export declare function setErrorClasses(classes: { GpuOutOfMemoryError?: new (message: string) => Error }): void
 export declare function synthRope(theta: number, rotDim: number, positions: number,
   yarn?: { factor: number; original_max_position_embeddings: number }): [Float32Array, Float32Array]
 export interface KvCacheOptions {

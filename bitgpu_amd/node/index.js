@@ -23,15 +23,29 @@ const V = 1
 const KSCALE = 2
 const VSCALE = 3
 
-class GpuOutOfMemoryError extends Error {}
+// The reference's error class (src/errors.ts:14-19: name 'GpuOutOfMemoryError'). A host that has
+// its own class (the engine's import of src/errors.ts) hands it to setErrorClasses, so its
+// `instanceof` checks match what this shim throws; this class stands in until then.
+class GpuOutOfMemoryError extends Error {
+  constructor(message) {
+    super(message)
+    this.name = 'GpuOutOfMemoryError'
+  }
+}
+let OomClass = GpuOutOfMemoryError
 
-// addon errors carry .code (BG_E_*) and .name; re-throw OOM as the reference's error class
+function setErrorClasses(classes) {
+  if (classes && typeof classes.GpuOutOfMemoryError === 'function') OomClass = classes.GpuOutOfMemoryError
+}
+
+// addon errors carry .code (BG_E_*) and .name; OOM is re-thrown as the host's error class
 function call(fn) {
   try {
     return fn()
   } catch (e) {
     if (e && e.name === 'GpuOutOfMemoryError') {
-      const oom = new GpuOutOfMemoryError(e.message)
+      const oom = new OomClass(e.message)
+      if (oom.name !== 'GpuOutOfMemoryError') oom.name = 'GpuOutOfMemoryError'
       oom.code = e.code
       throw oom
     }
@@ -98,4 +112,5 @@ function residMM(w, x, resid, out, stream = null) {
   call(() => addon.gemvResid(x, w.K, w.sign, w.scales, w.N || w.N0, resid, out, stream))
 }
 
-module.exports = { addon, KvCache, synthRope, fusedMM, residMM, GpuOutOfMemoryError, K, V, KSCALE, VSCALE, KV_DTYPE }
+module.exports = { addon, KvCache, synthRope, fusedMM, residMM, GpuOutOfMemoryError, setErrorClasses, K, V, KSCALE, VSCALE,
+  KV_DTYPE }

@@ -24,7 +24,13 @@
  *   - The decode kernel's split merge waits a bounded time for the partials of its own grid.
  *     If a wait gives up (the GPU shared with work that keeps the grid from running at once),
  *     that launch stores NaN and raises the cache's error word; the next bg_attention on the
- *     cache, or bg_stream_sync, returns BG_E_DEVICE once and resets the workspace.
+ *     cache, or bg_stream_sync, returns BG_E_DEVICE once and resets the workspace. Until then,
+ *     outputs of later launches on the cache may be wrong (a partial that lands after its
+ *     merger gave up can be taken by a later launch), not only NaN.
+ *   - When the device dispatches workgroups to its XCDs round robin (probed once per device at
+ *     bg_kv_create), the decode kernel exchanges the split partials of a kv head through one
+ *     XCD's L2. A merger that finds itself on another XCD raises the error word as above and
+ *     the library writes partials through to memory from then on.
  *
  * Storage modes mirror EngineOptions.kvCache (src/types.ts:143-154): f32, f16 (one RNE rounding
  * at write, shaders/copy_kv16.wgsl:13) and q8 (int8 codes + one f32 scale per 32 values,
@@ -97,6 +103,13 @@ int32_t bg_stream_sync(void* stream);
  * BG_E_UNSUPPORTED when the shape goes to another kernel. */
 int32_t bg_decode_plan(int32_t kv_heads, int32_t head_dim, int32_t dtype, int32_t S, int32_t H,
                        int32_t pos_base, int32_t num_cus, int32_t resident_per_cu, int32_t* out);
+
+/* Test hook with no counterpart in the reference: the decode split merge's poll bound
+ * (spin_limit polls before a merger gives up; 0 = the default, 2^20) and one split index that
+ * stores no partial (-1 = none), for every later bg_attention / bg_attention_noalloc call in
+ * the process. With a small bound and a withheld split the merge gives up while every kernel
+ * exits normally (the error path of the bounded wait, forced from the host). Host-only. */
+int32_t bg_debug_merge_hooks(int32_t spin_limit, int32_t withhold_split);
 
 /* Measurement aid with no counterpart in the reference: the streaming-read floor the decode
  * kernels are held against. `workgroups` workgroups of 512 threads each read one contiguous

@@ -252,6 +252,35 @@ def test_v2_snapshot_restores_into_a_wrapped_ring(dev, dtype):
         c.close()
 
 
+def test_restore_that_cannot_grow_writes_nothing(dev, monkeypatch):
+    """restoreCache grows the cache before it writes anything (src/engine.ts:2846-2848): when the
+    growth fails (host fault injector) it raises GpuOutOfMemoryError with the capacity and the
+    resident rows unchanged, and the same restore then succeeds. (A sink-mode cache holds its
+    whole window from creation, so only a plain cache grows here.)"""
+    rng = np.random.default_rng(67)
+    KV, D, n = 8, 128, 300
+    a = E.KvCache(1, KV, D, "q8", max_seq_len=1024, capacity=512)
+    k0 = rng.standard_normal((n, KV, D)).astype(np.float32)
+    fill_cache_raw(a, 0, k0, k0[::-1].copy())
+    snap = a.save_cache(ids=list(range(n + 1)))
+    b = E.KvCache(1, KV, D, "q8", max_seq_len=1024, capacity=64)
+    k1 = rng.standard_normal((40, KV, D)).astype(np.float32)
+    fill_cache_raw(b, 0, k1, k1)
+    before = export_k_v(b, 0, 0, 40)
+    monkeypatch.setenv("BG_FAULT_GROW_ALLOC", "1")
+    with pytest.raises(GpuOutOfMemoryError):
+        b.restore_cache(snap)
+    monkeypatch.delenv("BG_FAULT_GROW_ALLOC")
+    assert b.capacity == 64
+    for x, y in zip(before, export_k_v(b, 0, 0, 40)):
+        assert np.array_equal(x, y)
+    assert b.restore_cache(snap) == n
+    for x, y in zip(export_k_v(a, 0, 0, n), export_k_v(b, 0, 0, n)):
+        assert np.array_equal(x, y)
+    a.close()
+    b.close()
+
+
 @pytest.mark.parametrize("D", [128, 256])
 def test_q8_per_row_scale_mode(dev, D):
     """q8 with one scale per (position, kv head) row (bg_kv_set_q8_block(head_dim)): appendKV and

@@ -1,5 +1,5 @@
 """GPU: the decode kernel's split merge fails loudly. A host-set test hook makes one split store
-no partial and bounds the mergers' wait to a few rounds, so the merge gives up while every
+no partial and bounds the mergers' wait to a few rounds (bg_debug_merge_hooks), so the merge gives up while every
 kernel still exits normally; the launch stores NaN, and the next bg_attention on the cache (or
 bg_stream_sync) returns BG_E_DEVICE once, after resetting the split workspace. Later launches
 match the oracle again."""
@@ -30,18 +30,18 @@ def _case(dtype, L=8192, seed=71):
 
 
 @pytest.mark.parametrize("dtype,report", [("q8", "attention"), ("f16", "stream_sync")])
-def test_merge_timeout_is_reported(dev, monkeypatch, dtype, report):
+def test_merge_timeout_is_reported(dev, dtype, report):
     c, q, exp, H = _case(dtype)
     L = 8192
     good = E.attention(c, 0, q, 1, H, L - 1)
     torch.cuda.synchronize()
     assert rel_err(good.cpu().numpy(), exp) <= 2e-3
-    monkeypatch.setenv("BG_DEBUG_WITHHOLD_SPLIT", "1")
-    monkeypatch.setenv("BG_DEBUG_MERGE_SPIN", "32")
-    bad = E.attention(c, 0, q, 1, H, L - 1)          # enqueued fine: the failure is on the GPU
-    torch.cuda.synchronize()
-    monkeypatch.delenv("BG_DEBUG_WITHHOLD_SPLIT")
-    monkeypatch.delenv("BG_DEBUG_MERGE_SPIN")
+    _lib.check(_lib.lib().bg_debug_merge_hooks(32, 1))  # a poll bound of 32 rounds, split 1 withheld
+    try:
+        bad = E.attention(c, 0, q, 1, H, L - 1)      # enqueued fine: the failure is on the GPU
+        torch.cuda.synchronize()
+    finally:
+        _lib.check(_lib.lib().bg_debug_merge_hooks(0, -1))
     assert np.isnan(bad.cpu().numpy()).all()          # every unit waits on the withheld split
     with pytest.raises(BitgpuError, match="gave up waiting") as ei:
         if report == "attention":

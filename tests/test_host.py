@@ -136,9 +136,9 @@ def _snap(**kw):
 _MODEL = {"layers": 2, "kvHeads": 8, "headDim": 128, "hidden": 0, "vocab": 0}
 
 
-def _validate(snap, roll=True, sinks=4, kv="f16", model=_MODEL, max_seq=4100, cache_len=0, history=()):
+def _validate(snap, roll=True, sinks=4, kv="f16", model=_MODEL, max_seq=4100, cache_len=0, history=(), hybrid=False):
     return E.validate_snapshot(snap, roll=roll, sinks=sinks, kv_cache=kv, model=model, max_seq_len=max_seq,
-                               data_bytes=100, cache_len=cache_len, history=history)
+                               data_bytes=100, cache_len=cache_len, history=history, hybrid=hybrid)
 
 
 @pytest.mark.parametrize("snap,kw,msg", [
@@ -172,6 +172,24 @@ def test_restore_lengths_and_delta_prefix():
         _validate(d, roll=False, cache_len=12, history=list(range(12)))
     with pytest.raises(_lib.BitgpuError, match=r"prefix does not match the current prewarm \(token 3\)"):
         _validate(d, roll=False, cache_len=10, history=[0, 1, 2, 7, 4, 5, 6, 7, 8, 9])
+
+
+def test_restore_rejects_delta_on_the_hybrid_backbone():
+    """restoreCache rejects a delta snapshot (base > 0) on the qwen3_5 hybrid backbone
+    (src/engine.ts:2828), after the length and before the slot and size checks; a full
+    snapshot (base 0) restores there as on a dense model."""
+    d = _snap(version=1, roll=None, base=10, data=b"\0" * 3900)
+    with pytest.raises(_lib.BitgpuError, match="delta snapshots are not supported for the qwen3_5 hybrid backbone"):
+        _validate(d, roll=False, cache_len=10, history=list(range(10)), hybrid=True)
+    # the reference's order: this check precedes the slot check (a delta that also overflows
+    # maxSeqLen reports the hybrid rejection) and follows the empty-ids check
+    with pytest.raises(_lib.BitgpuError, match="qwen3_5 hybrid backbone"):
+        _validate(d, roll=False, cache_len=10, history=list(range(10)), hybrid=True, max_seq=20)
+    with pytest.raises(_lib.BitgpuError, match="holds no tokens"):
+        _validate(_snap(version=1, roll=None, base=10, ids=[]), roll=False, hybrid=True)
+    full = _snap(version=1, roll=None, data=b"\0" * 4900)
+    assert _validate(full, roll=False, hybrid=True) == (49, 0, 49)
+    assert _validate(d, roll=False, cache_len=10, history=list(range(10)), hybrid=False) == (49, 10, 39)
 
 
 # ---------------------------------------------------------------- decode split plan

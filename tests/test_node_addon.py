@@ -10,6 +10,7 @@ import numpy as np
 import pytest
 
 from bitgpu_amd import engine as E
+from bitgpu_amd import _lib
 from bitgpu_amd._lib import BG_E_UNSUPPORTED
 from oracle import ref
 
@@ -18,10 +19,11 @@ NODE_DIR = os.path.join(ROOT, "bitgpu_amd", "node")
 NODE = shutil.which("node")
 
 
-def run_node(script, tmp_path, timeout=120):
+def run_node(script, tmp_path, timeout=120, env=None):
     p = tmp_path / "t.js"
     p.write_text(f"const b = require({json.dumps(os.path.join(NODE_DIR, 'index.js'))});\n" + script)
-    r = subprocess.run([NODE, str(p)], capture_output=True, text=True, timeout=timeout)
+    r = subprocess.run([NODE, str(p)], capture_output=True, text=True, timeout=timeout,
+                       env=None if env is None else {**os.environ, **env})
     assert r.returncode == 0, r.stderr
     return r.stdout
 
@@ -119,3 +121,36 @@ console.log(JSON.stringify(res))
     assert res["s2"] == [0, 12345]
     assert res["err"][0] == BG_E_UNSUPPORTED
     assert "32 or head_dim 128" in res["err"][1]
+
+
+@pytest.mark.gpu
+@pytestmark_node
+def test_addon_oom_is_the_reference_error_class(tmp_path):
+    """A failed KV growth (the host fault injector makes its first device allocation fail)
+    reaches JS as the reference's GpuOutOfMemoryError (src/errors.ts:14-19): name
+    'GpuOutOfMemoryError', instanceof the shim's class, and instanceof the host's own class once
+    the host has passed it to setErrorClasses. The cache keeps its capacity."""
+    out = run_node("""
+const res = {}
+const c = new b.KvCache({layers: 1, kvHeads: 8, headDim: 128, kvCache: 'f16', maxSeqLen: 4096, capacity: 64})
+try { c.ensureKvCapacity(1000) } catch (e) {
+  res.shim = [e instanceof b.GpuOutOfMemoryError, e instanceof Error, e.name, e.code, e.message]
+}
+class HostOom extends Error { constructor(m) { super(m); this.name = 'GpuOutOfMemoryError' } }
+b.setErrorClasses({GpuOutOfMemoryError: HostOom})
+try { c.ensureKvCapacity(1000) } catch (e) {
+  res.host = [e instanceof HostOom, e.name, e.code]
+}
+res.cap = c.capacity
+c.dispose()
+try { new b.KvCache({layers: 1, kvHeads: 8, headDim: 128, maxSeqLen: 60, overflow: 'sinks'}) } catch (e) {
+  res.other = [e instanceof HostOom, e.name]
+}
+console.log(JSON.stringify(res))
+""", tmp_path, env={"BG_FAULT_GROW_ALLOC": "1"})
+    res = json.loads(out.strip().splitlines()[-1])
+    assert res["shim"][:4] == [True, True, "GpuOutOfMemoryError", _lib.BG_E_OOM]
+    assert "KV cache growth" in res["shim"][4]
+    assert res["host"] == [True, "GpuOutOfMemoryError", _lib.BG_E_OOM]
+    assert res["cap"] == 64
+    assert res["other"] == [False, "Error"]        # only OOM maps to the class
