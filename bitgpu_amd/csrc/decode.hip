@@ -802,8 +802,13 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
   // Mergers are the highest split indices, so workgroups are dispatched before the mergers that
   // wait on them; the host also sizes the grid to fit the GPU at once. The wait is bounded
   // (p.spin_limit rounds): a merger that gives up stores NaN and raises p.err.
-  // Thread (k, c) holds float4 column c of splits k, k + KG, .. (MAXL at a time); wave 0 also
-  // holds (m, l) of every split, one per lane.
+  // Thread (k, c) holds float4 column c of splits k, k + KG, .. (MAXL at a time); every wave
+  // also holds (m, l) of every split, one per lane, and derives the log-sum-exp maximum, sum and
+  // weights itself (the same DPP reductions in every wave, so the weights agree bit for bit):
+  // a thread takes its splits' weights from their lanes by ds_bpermute instead of from LDS
+  // behind a barrier. The empty markers go back as each batch is consumed, with the split in
+  // the scalar offset so that consecutive stores share their address registers (a register
+  // rewritten under a pending store makes the compiler wait for that store's acknowledgement).
   constexpr int KG = NTHR / 16;                // split groups
   // o slots per thread and batch (KG * MAXL splits a batch: 64 on 4 waves); 5 for the D=256
   // one-tile kernel (4 waves, 80 a batch), whose 8193-8448-slot contexts (257-264 tiles) take
@@ -812,8 +817,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
   constexpr int MAXL = (ONE && D == 256) ? 5 : 4;
   constexpr int MLC = (kMaxSplits + 63) / 64;  // (m, l) slots per lane of wave 0
   const int c = tid & 15, k = tid >> 4;
-  float* wts = (float*)smem;                                   // [NS]
-  float4* red = (float4*)(smem + (((size_t)NS * 4 + 15) & ~(size_t)15));  // [NW][16]
+  float4* red = (float4*)smem;                                 // [NW][16]
   const u32x4v empty4 = {kPartialEmpty, kPartialEmpty, kPartialEmpty, kPartialEmpty};
   bool gave_up = false;  // workgroup-uniform (every exit of poll is a block-wide vote)
   for (int u = split - first_merger; u < units; u += p.n_mergers) {
@@ -833,7 +837,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
           v[i] = sp < NS ? __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(wrs, (ubase + sp * kUnitF4 + c) * 16, 0, kSC1))
                          : floatx4{0.f, 0.f, 0.f, 0.f};
         }
-        if (with_ml && wave == 0) {
+        if (with_ml) {
 #pragma unroll
           for (int j = 0; j < MLC; j++) {
             const int sp = 64 * j + lane;
@@ -854,24 +858,35 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
       }
       return false;
     };
+    // the weights of every split, one per lane of every wave: w[j] at lane l is split 64 j + l
+    float w[MLC];
     // consume a batch: weighted sum, then mark its slots empty again
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    const int vo = (ubase + k * kUnitF4 + c) * 16;
     auto consume = [&](int b0) {
 #pragma unroll
       for (int i = 0; i < MAXL; i++) {
         const int sp = b0 + k + KG * i;
+        // the weight of split sp from lane sp % 64 of w[sp / 64]
+        float wi = 0.0f;
+#pragma unroll
+        for (int j = 0; j < MLC; j++) {
+          if (64 * j < NS) {
+            const float t = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * (sp & 63), __float_as_int(w[j])));
+            wi = (sp >> 6) == j ? t : wi;
+          }
+        }
         if (sp < NS) {
-          const float w = wts[sp];
-          acc.x += v[i][0] * w;
-          acc.y += v[i][1] * w;
-          acc.z += v[i][2] * w;
-          acc.w += v[i][3] * w;
-          __builtin_amdgcn_raw_buffer_store_b128(empty4, wrs, (ubase + sp * kUnitF4 + c) * 16, 0, kSC1);
+          acc.x += v[i][0] * wi;
+          acc.y += v[i][1] * wi;
+          acc.z += v[i][2] * wi;
+          acc.w += v[i][3] * wi;
+          __builtin_amdgcn_raw_buffer_store_b128(empty4, wrs, vo, (b0 + KG * i) * kUnitF4 * 16, kSC1);
         }
       }
     };
     gave_up = !poll(0, true) || gave_up;
-    if (wave == 0) {
+    {
       float M = -INFINITY;
 #pragma unroll
       for (int j = 0; j < MLC; j++) M = fmaxf(M, ml[j].x);
@@ -881,15 +896,14 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
       for (int j = 0; j < MLC; j++) lt += ml[j].y * __builtin_amdgcn_exp2f(ml[j].x - M);
       lt = wave_sum(lt);
 #pragma unroll
-      for (int j = 0; j < MLC; j++) {
-        const int sp = 64 * j + lane;
-        if (sp < NS) {
-          wts[sp] = __builtin_amdgcn_exp2f(ml[j].x - M) / lt;
-          __builtin_amdgcn_raw_buffer_store_b128(empty4, wrs, (ubase + sp * kUnitF4 + 16) * 16, 0, kSC1);
-        }
+      for (int j = 0; j < MLC; j++) w[j] = __builtin_amdgcn_exp2f(ml[j].x - M) / lt;
+      if (wave == 0) {
+        const int vm = (ubase + lane * kUnitF4 + 16) * 16;
+#pragma unroll
+        for (int j = 0; j < MLC; j++)
+          if (64 * j + lane < NS) __builtin_amdgcn_raw_buffer_store_b128(empty4, wrs, vm, 64 * j * kUnitF4 * 16, kSC1);
       }
     }
-    __syncthreads();
     consume(0);
     for (int b0 = KG * MAXL; b0 < NS; b0 += KG * MAXL) {
       gave_up = !poll(b0, false) || gave_up;
@@ -1118,7 +1132,7 @@ static hipError_t launch_cfg(const LayerView& L, const AttnArgs& a, hipStream_t 
   const int NP = (R + PR - 1) / PR;
   size_t smem = SM::total(NP, R);
   if (smem != decode_lds_bytes(D, DT, R, NW, PR)) return hipErrorInvalidValue;  // the two plans agree
-  // the merge reuses the space: weights [NS] (16-byte aligned) and [waves][16] float4
+  // the merge reuses the space ([waves][16] float4; the bound keeps an older, larger plan)
   const size_t merge_max = (((size_t)kMaxSplits * 4 + 15) & ~(size_t)15) + (size_t)NW * 16 * 16;
   smem = smem > merge_max ? smem : merge_max;
   if (smem > kDecodeLdsMax) return hipErrorInvalidValue;

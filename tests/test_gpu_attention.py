@@ -178,10 +178,20 @@ def test_decode_workspace_reuse(dev, dtype):
 
 
 # ------------------------------------------------------------------ f32 kernel
-# (1, 1500) and (3, 4100): the split kernel with 24 and 65 splits a kv head, past one merge batch
+# The split kernel plans ceil(64-slot tiles x kv heads / CUs) tiles a split (one workgroup a CU
+# on the 256-CU gfx950): (1, 1500) gives 24 splits a kv head, (3, 4100) 65 tiles two a split,
+# 33 splits -- past one merge batch of 16 and past two
 @pytest.mark.parametrize("S,L", [(1, 1), (1, 100), (7, 40), (64, 64), (1, 1500), (3, 4100)])
 def test_f32_kernel(dev, S, L):
     out, exp = _raw_case("f32", 16, 4, 128, L, S, seed=S * 1000 + L)
+    _check("f32", out, exp)
+
+
+@pytest.mark.parametrize("S", [1, 2])
+def test_f32_kernel_many_splits(dev, S):
+    """One kv head (4 query heads) over 4100 slots: 65 tiles take one split each, 65 splits a
+    kv head, five batches of the f32 merge."""
+    out, exp = _raw_case("f32", 4, 1, 128, 4100, S, seed=77 + S)
     _check("f32", out, exp)
 
 
