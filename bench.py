@@ -16,6 +16,7 @@ Only one GPU is used: --gpus above 1 exits with a message.
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import json
 import os
 import sys
@@ -28,6 +29,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 MFMA_F16_PEAK_TFLOPS = 2516.6  # MI355X dense fp16/bf16 MFMA
+F32_PEAK_TFLOPS = 157.3        # MI355X fp32 (matrix and vector)
 
 
 def c3_bytes(L, KV=8, D=128, H=32):
@@ -581,6 +583,12 @@ def main():
                                          "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
         extra["c2_prefill_f16"] = bench_prefill(torch, E, W, W.C2, W.C2_S, max(3, args.steps // 2), args.warmup, 2)
         extra["c5_prefill_q8"] = bench_prefill(torch, E, W, W.C5, W.C5_PREFILL, 3, 1, 5)
+        # the C2 shape with the reference's default f32 storage, on the f32 matrix cores
+        pf32 = bench_prefill(torch, E, W, dataclasses.replace(W.C2, kv="f32"), W.C2_S, max(3, args.steps // 4),
+                             args.warmup, 2)
+        pf32["fp32_frac"] = round(pf32["tflops"] / F32_PEAK_TFLOPS, 4)
+        del pf32["mfma_frac"]
+        extra["c2_prefill_f32"] = pf32
         extra["c5_decode_q8"] = bench_c5_decode(torch, E, W, args.steps, args.warmup)
         extra["c1_decode_f32"] = bench_c1(torch, E, W, args.steps, args.warmup)
         extra["c4_sinks_f16"] = bench_c4(torch, E, W, args.steps, args.warmup)

@@ -105,6 +105,28 @@ def test_e2e_c2_prefill(dev):
     c.close()
 
 
+# ------------------------------------------------------------------ C2 shape with f32 storage
+def test_e2e_c2_prefill_f32(dev):
+    """The C2 prefill (S=2048, H32/KV8/D128) with the reference's default f32 storage: the f32
+    matrix-core prefill against the oracle at max-abs 1e-4."""
+    cfg, S = W.C2, W.C2_S
+    q, k, v, _ = W.prefill_inputs(cfg, S, seed=12)
+    cos_d, sin_d, _, _ = rope_dev(cfg.theta, cfg.rot, S)
+    ones = t(np.ones(cfg.D, np.float32))
+    c = E.KvCache(1, cfg.KV, cfg.D, "f32", max_seq_len=S, capacity=S)
+    qr = E.qkv_prologue(c, 0, t(q), t(k), t(v), S, cfg.H, ones, ones, cfg.eps, cos_d, sin_d, cfg.rot, 0, 0)
+    out = E.attention(c, 0, qr, S, cfg.H, 0)
+    torch.cuda.synchronize()
+    cos, sin = _oracle_tables(cfg, S)
+    onesh = np.ones(cfg.D, np.float32)
+    qn = ref.norm_rope(q, onesh, cfg.eps, cos, sin, np.arange(S))
+    kn = ref.norm_rope(k, onesh, cfg.eps, cos, sin, np.arange(S))
+    _check_q(qr, qn)
+    kk, vv = _check_stored(c, 0, 0, kn, v)
+    _check_out("f32", out.cpu().numpy(), ref.attention(qn, kk, vv, 0))
+    c.close()
+
+
 # ------------------------------------------------------------------ C3: q8 decode at 4k/16k/32k
 @pytest.mark.parametrize("L", W.C3_CONTEXTS)
 def test_e2e_c3_decode(dev, L):
