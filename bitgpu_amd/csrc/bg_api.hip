@@ -55,9 +55,9 @@ struct bg_kv_cache {
   // snapshot staging buffer (grown on demand, kept until destroy)
   void* stage = nullptr;
   size_t stage_bytes = 0;
-  // fused decode projection: raw K and V rows [2 KV D] and the per-head arrival counters
+  // fused decode projection: the gather buffer of raw rows [kProjMaxHeads][D], the empty marker
+  // in every value between launches
   float* proj_raw = nullptr;
-  unsigned* proj_count = nullptr;
 };
 
 namespace {
@@ -214,6 +214,8 @@ int32_t take_merge_error(bg_kv_cache* c, hipStream_t st) {
     e = hipMemsetD32((hipDeviceptr_t)c->ws, (int)bg::decode_workspace_empty(), c->ws_floats);
   for (const auto& r : c->retired_ws)
     if (e == hipSuccess) e = hipMemsetD32((hipDeviceptr_t)r.first, (int)bg::decode_workspace_empty(), r.second);
+  if (e == hipSuccess && c->proj_raw)
+    e = hipMemsetD32((hipDeviceptr_t)c->proj_raw, (int)bg::kWorkspaceEmpty, bg::qkv_proj_raw_floats(kProjMaxHeads, c->D));
   int dev = 0;
   if (e == hipSuccess) e = hipGetDevice(&dev);
   if (e == hipSuccess && dev >= 0 && dev < kMaxDevices) {
@@ -445,13 +447,13 @@ int32_t bg_kv_create(int32_t n_layers, int32_t kv_heads, int32_t head_dim, int32
   }
   hipError_t e = hipHostMalloc((void**)&c->err_host, 64, hipHostMallocMapped | hipHostMallocCoherent);
   if (e == hipSuccess) e = hipHostGetDevicePointer((void**)&c->err_dev, c->err_host, 0);
-  if (e == hipSuccess) e = hipMalloc((void**)&c->proj_raw, (size_t)2 * kv_heads * head_dim * sizeof(float));
-  if (e == hipSuccess) e = hipMalloc((void**)&c->proj_count, (size_t)kProjMaxHeads * bg::kCounterStride * sizeof(unsigned));
-  if (e == hipSuccess) e = hipMemset(c->proj_count, 0, (size_t)kProjMaxHeads * bg::kCounterStride * sizeof(unsigned));
+  const size_t praw = bg::qkv_proj_raw_floats(kProjMaxHeads, head_dim);
+  if (e == hipSuccess) e = hipMalloc((void**)&c->proj_raw, praw * sizeof(float));
+  if (e == hipSuccess) e = hipMemsetD32((hipDeviceptr_t)c->proj_raw, (int)bg::kWorkspaceEmpty, praw);
+  if (e == hipSuccess) e = hipDeviceSynchronize();
   if (e != hipSuccess) {
     if (c->err_host) (void)hipHostFree(c->err_host);
     if (c->proj_raw) (void)hipFree(c->proj_raw);
-    if (c->proj_count) (void)hipFree(c->proj_count);
     free_layers(c->k, c->v, c->ks, c->vs);
     delete c;
     return hip_fail(e, "KV cache side buffers allocation");
@@ -475,7 +477,6 @@ int32_t bg_kv_destroy(bg_kv_cache* c) {
   if (c->err_host) (void)hipHostFree(c->err_host);
   if (c->stage) (void)hipFree(c->stage);
   if (c->proj_raw) (void)hipFree(c->proj_raw);
-  if (c->proj_count) (void)hipFree(c->proj_count);
   free_layers(c->k, c->v, c->ks, c->vs);
   if (c->ws) (void)hipFree(c->ws);
   if (c->ws_count) (void)hipFree(c->ws_count);
@@ -960,8 +961,11 @@ int32_t bg_qkv_proj_prologue(bg_kv_cache* c, int32_t layer, const float* x, int3
   a.pos = pos;
   a.slot = slot;
   a.q_out = q_out;
-  a.kv_raw = c->proj_raw;
-  a.count = c->proj_count;
+  a.raw = c->proj_raw;
+  a.err = c->err_dev;
+  a.spin_limit = g_merge_spin.load(std::memory_order_relaxed);
+  const int xs = xcd_state(c->device);
+  a.n_xcd = xs > 0 ? xs : 0;
   hipError_t e = bg::launch_qkv_proj(view(c, layer), a, (hipStream_t)stream);
   return e == hipSuccess ? BG_OK : hip_fail(e, "qkv projection launch");
 }

@@ -70,10 +70,15 @@ struct QkvProjArgs {
   const float* q_gamma; const float* k_gamma; float eps;
   const float* cos_tab; const float* sin_tab; int rot_dim;
   int pos, slot;
-  float* q_out;                    // [H, D]: raw rows first, then the normed, roped rows
-  float* kv_raw;                   // [2 KV D] raw K and V rows
-  unsigned* count;                 // [H + 2 KV] arrival counters kCounterStride apart, zero between launches
+  float* q_out;                    // [H, D] normed, roped rows
+  float* raw;                      // [H + 2 KV][D] raw rows a head's finishing workgroup gathers;
+                                   // every value the empty marker (kWorkspaceEmpty) between launches
+  unsigned* err;                   // host-visible error word: a finisher's bounded wait gave up
+  int spin_limit;                  // poll rounds before a finisher gives up (0: 2^20)
+  int n_xcd;                       // > 0: workgroups go to XCDs round robin (see AttnArgs)
 };
+// raw-row floats the fused projection's gather buffer holds (heads of every kind x head_dim)
+size_t qkv_proj_raw_floats(int heads, int D);
 // Arrival counters (the fused projection's per head, the f32 decode's per kv head) sit 256 bytes
 // apart: 384 workgroups' atomics on counters packed into two lines serialize (the 8B-shape qkv
 // projection took 8.6 us with them packed, 7.5 us apart).
