@@ -869,7 +869,7 @@ int32_t bg_attention_noalloc(bg_kv_cache* c, int32_t layer, const float* q, int3
   LayerView L = view(c, layer);
   bg::AttnArgs a = attention_args(c, q, S, H, pos_base, scale, gate, gate_stride, out);
   if (c->dtype == BG_KV_F32) {
-    // the exact-f32 kernel of one wave per (query, head) keeps no partials
+    // the f32 kernels run without partials here (the matrix-core kernel for every shape)
     e = bg::launch_attention_f32(L, a, st);
   } else if (bg::decode_preferred(L, S, H)) {
     bg::DecodePlan pl;

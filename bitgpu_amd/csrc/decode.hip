@@ -819,7 +819,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
   const int c = tid & 15, k = tid >> 4;
   float4* red = (float4*)smem;                                 // [NW][16]
   const u32x4v empty4 = {kPartialEmpty, kPartialEmpty, kPartialEmpty, kPartialEmpty};
-  bool gave_up = false;  // workgroup-uniform (every exit of poll is a block-wide vote)
+  bool gave_up = false;  // wave-uniform; workgroup-uniform after each unit's reduction vote
   for (int u = split - first_merger; u < units; u += p.n_mergers) {
     const int rho = u / UPR, d0 = (u % UPR) * 64;
     const int ubase = u * NS * kUnitF4;
@@ -853,7 +853,9 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
         for (int i = 0; i < MAXL; i++)
 #pragma unroll
           for (int e = 0; e < 4; e++) missing = missing || __float_as_uint(v[i][e]) == kPartialEmpty;
-        if (!__syncthreads_or(missing)) return true;
+        // a vote of this wave only: every wave holds every (m, l) and polls its own o slots,
+        // so the waves meet once, at the reduction below
+        if (!__any(missing)) return true;
         __builtin_amdgcn_s_sleep(1);
       }
       return false;
@@ -897,12 +899,6 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
       lt = wave_sum(lt);
 #pragma unroll
       for (int j = 0; j < MLC; j++) w[j] = __builtin_amdgcn_exp2f(ml[j].x - M) / lt;
-      if (wave == 0) {
-        const int vm = (ubase + lane * kUnitF4 + 16) * 16;
-#pragma unroll
-        for (int j = 0; j < MLC; j++)
-          if (64 * j + lane < NS) __builtin_amdgcn_raw_buffer_store_b128(empty4, wrs, vm, 64 * j * kUnitF4 * 16, kSC1);
-      }
     }
     consume(0);
     for (int b0 = KG * MAXL; b0 < NS; b0 += KG * MAXL) {
@@ -922,7 +918,14 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
       }
     }
     if (lane < 16) red[wave * 16 + c] = acc;
-    __syncthreads();
+    gave_up = __syncthreads_or(gave_up);
+    // every wave has read every (m, l): wave 0 marks those slots empty again
+    if (wave == 0) {
+      const int vm = (ubase + lane * kUnitF4 + 16) * 16;
+#pragma unroll
+      for (int j = 0; j < MLC; j++)
+        if (64 * j + lane < NS) __builtin_amdgcn_raw_buffer_store_b128(empty4, wrs, vm, 64 * j * kUnitF4 * 16, kSC1);
+    }
     if (tid < 16) {
 #pragma unroll
       for (int w = 1; w < NW; w++) {
