@@ -733,61 +733,50 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
   const int units = p.R * UPR;
   const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(p.ws + (size_t)kvh * units * NS * kUnitF4), (short)0, 0x7fffffff, 0x00020000);
-  // Each float4 column of the R x D partial is summed by 4 adjacent lanes (NW/4 waves each,
-  // all LDS reads independent) whose sums meet by DPP; the first lane of the four stores it.
-  constexpr int WPT = NW / 4;
-  const int q4 = tid & 3;
-  for (int c = tid >> 2; c < C4; c += NTHR / 4) {
-    const int rho = c / (D / 4), d = 4 * (c % (D / 4));
-    float4 v[WPT];
-    float lv[WPT], mv[WPT];
+  // Each float4 column of the R x D partial is summed over the waves by one thread, every LDS
+  // read of the column independent of the others; the column loop has a compile-time trip bound
+  // and is unrolled, so a thread's columns are read together.
+  constexpr int CMAX = (RS * (D / 4) + NTHR - 1) / NTHR;
 #pragma unroll
-    for (int j = 0; j < WPT; j++) {
-      const int w = q4 * WPT + j;
-      v[j] = *(const float4*)(ow + ((size_t)w * p.R + rho) * DP + d);
-      lv[j] = lw[w * p.R + rho];
-      mv[j] = s_mw[w][rho];
-    }
-    float4 acc = v[0];
-    float lt = lv[0], mx = mv[0];
+  for (int j = 0; j < CMAX; j++) {
+    const int c = tid + j * NTHR;
+    if (c < C4) {
+      const int rho = c / (D / 4), d = 4 * (c % (D / 4));
+      float4 acc = *(const float4*)(ow + (size_t)rho * DP + d);
+      float lt = lw[rho], mx = s_mw[0][rho];
 #pragma unroll
-    for (int j = 1; j < WPT; j++) {
-      acc.x += v[j].x;
-      acc.y += v[j].y;
-      acc.z += v[j].z;
-      acc.w += v[j].w;
-      lt += lv[j];
-      mx = fmaxf(mx, mv[j]);
-    }
-    acc.x = group_sum<4>(acc.x);
-    acc.y = group_sum<4>(acc.y);
-    acc.z = group_sum<4>(acc.z);
-    acc.w = group_sum<4>(acc.w);
-    lt = group_sum<4>(lt);
-    mx = group_max<4>(mx);
-    if (q4 != 0) continue;
-    if (single) {
-      const int s = rho / p.G, h = kvh * p.G + rho % p.G;
-      float r[4] = {acc.x / lt, acc.y / lt, acc.z / lt, acc.w / lt};
-      if (p.gate) {
-        const float* gr = p.gate + ((size_t)s * p.H + h) * p.gate_stride + d;
-#pragma unroll
-        for (int e = 0; e < 4; e++) r[e] = r[e] / (1.0f + expf(-gr[e]));
+      for (int w = 1; w < NW; w++) {
+        const float4 v = *(const float4*)(ow + ((size_t)w * p.R + rho) * DP + d);
+        acc.x += v.x;
+        acc.y += v.y;
+        acc.z += v.z;
+        acc.w += v.w;
+        lt += lw[w * p.R + rho];
+        mx = fmaxf(mx, s_mw[w][rho]);
       }
-      *(float4*)(p.out + ((size_t)s * p.H + h) * D + d) = make_float4(r[0], r[1], r[2], r[3]);
-    } else if (split != p.withhold_split) {
-      const int slot = ((rho * UPR + d / 64) * NS + split) * kUnitF4;
-      if (p.xcd_local > 0) {  // into the XCD's L2 (see xcd_local)
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4v, acc), wrs, (slot + (d % 64) / 4) * 16, 0, 0);
-        if (d % 64 == 0) {
-          const float4 ml = make_float4(mx, lt, 0.0f, 0.0f);
-          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4v, ml), wrs, (slot + 16) * 16, 0, 0);
+      if (single) {
+        const int s = rho / p.G, h = kvh * p.G + rho % p.G;
+        float r[4] = {acc.x / lt, acc.y / lt, acc.z / lt, acc.w / lt};
+        if (p.gate) {
+          const float* gr = p.gate + ((size_t)s * p.H + h) * p.gate_stride + d;
+#pragma unroll
+          for (int e = 0; e < 4; e++) r[e] = r[e] / (1.0f + expf(-gr[e]));
         }
-      } else {
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4v, acc), wrs, (slot + (d % 64) / 4) * 16, 0, kSC1);
-        if (d % 64 == 0) {
-          const float4 ml = make_float4(mx, lt, 0.0f, 0.0f);
-          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4v, ml), wrs, (slot + 16) * 16, 0, kSC1);
+        *(float4*)(p.out + ((size_t)s * p.H + h) * D + d) = make_float4(r[0], r[1], r[2], r[3]);
+      } else if (split != p.withhold_split) {
+        const int slot = ((rho * UPR + d / 64) * NS + split) * kUnitF4;
+        if (p.xcd_local > 0) {  // into the XCD's L2 (see xcd_local)
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4v, acc), wrs, (slot + (d % 64) / 4) * 16, 0, 0);
+          if (d % 64 == 0) {
+            const float4 ml = make_float4(mx, lt, 0.0f, 0.0f);
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4v, ml), wrs, (slot + 16) * 16, 0, 0);
+          }
+        } else {
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4v, acc), wrs, (slot + (d % 64) / 4) * 16, 0, kSC1);
+          if (d % 64 == 0) {
+            const float4 ml = make_float4(mx, lt, 0.0f, 0.0f);
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4v, ml), wrs, (slot + 16) * 16, 0, kSC1);
+          }
         }
       }
     }
