@@ -162,12 +162,12 @@ struct DecodeSmem {
   static constexpr size_t p_bytes_wave = (size_t)NBV * RS * 32 * 2;
   static constexpr size_t c_bytes_wave = (size_t)RS * 4;
   static constexpr int DP = D + 4;                        // padded row of a wave partial
-  __host__ __device__ static size_t merge_bytes(int R) { return (size_t)NW * R * (DP + 1) * 4; }
-  __host__ __device__ static size_t total(int np, int R) {
-    size_t a = q_bytes(np) + NW * (p_bytes_wave + c_bytes_wave);
-    size_t b = merge_bytes(R);
-    return a > b ? a : b;
+  // a wave's part: its P tiles and corrections in the tile loop, then its raw o rows
+  __host__ __device__ static size_t wave_bytes(int R) {
+    const size_t t = p_bytes_wave + c_bytes_wave, o = (size_t)R * DP * 4;
+    return t > o ? t : o;
   }
+  __host__ __device__ static size_t total(int np, int R) { return q_bytes(np) + NW * wave_bytes(R); }
 };
 
 // One wave's raw loads for a 32-slot tile (kept in flight while the previous tile computes).
@@ -302,7 +302,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
 
   uint4* qs = (uint4*)smem;                                           // [NP][NT][2][64]
   unsigned char* pbase = smem + SM::q_bytes(NP);
-  _Float16* pl = (_Float16*)(pbase + wave * (SM::p_bytes_wave + SM::c_bytes_wave));  // [NBV][RS][32]
+  _Float16* pl = (_Float16*)(pbase + wave * SM::wave_bytes(p.R));  // [NBV][RS][32]
   float* cl = (float*)((unsigned char*)pl + SM::p_bytes_wave);                         // [RS]
 
   const Ring ring = p.L.ring;
@@ -673,30 +673,13 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
   }
 
   // ---------------- combine the waves of the workgroup ----------------
-  // The row maxima go through an LDS array of their own (the tile loop never touches it), so
-  // one barrier publishes them and ends every wave's use of the tile-loop space. Each wave then
-  // rescales its own o and l to the workgroup maximum of the row and stores them as float4
-  // (rows padded by 4 floats to spread the banks); the sum over the waves is plain adds.
-  __shared__ float s_mw[NW][RS];
-#pragma unroll
-  for (int pass = 0; pass < NPK; pass++) {
-    if (pass >= NP) break;
-#pragma unroll
-    for (int i = 0; i < RL; i++) {
-      const int rho = row_of(pass, i);
-      if (n == 0 && rho < p.R) s_mw[wave][rho] = m[pass][i];
-    }
-  }
-  __syncthreads();
+  // Each wave leaves its raw partial (no rescaling, so nothing to wait for) in its own part of
+  // LDS: the row maxima and sums in two small arrays the tile loop never touches, the o rows
+  // (padded by 4 floats to spread the banks) over its own P tiles, which no other wave reads;
+  // one barrier publishes them. The sum over the waves (below) rescales to the workgroup maximum.
+  __shared__ float s_mw[NW][RS], s_lw[NW][RS];
   constexpr int DP = SM::DP;
-  float* lw = (float*)smem;               // [NW][R]
-  float* ow = lw + NW * p.R;              // [NW][R][DP]
-  auto row_max = [&](int rho) {
-    float M = s_mw[0][rho];
-#pragma unroll
-    for (int w = 1; w < NW; w++) M = fmaxf(M, s_mw[w][rho]);
-    return M;
-  };
+  const size_t wbytes = SM::wave_bytes(p.R);
 #pragma unroll
   for (int pass = 0; pass < NPK; pass++) {
     if (pass >= NP) break;
@@ -704,23 +687,25 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     for (int i = 0; i < RL; i++) {
       const float lt = group16_sum(lsum[pass][i]);
       const int rho = row_of(pass, i);
-      if (n == 0 && rho < p.R) lw[wave * p.R + rho] = lt * __builtin_amdgcn_exp2f(m[pass][i] - row_max(rho));
+      if (n == 0 && rho < p.R) {
+        s_mw[wave][rho] = m[pass][i];
+        s_lw[wave][rho] = lt;
+      }
     }
   }
 #pragma unroll
   for (int st = 0; st < NSET; st++) {
     const int rho = 16 * st + n;
     if (rho < p.R) {
-      const float f = __builtin_amdgcn_exp2f(s_mw[wave][rho] - row_max(rho));
-      float* orow = ow + ((size_t)wave * p.R + rho) * DP + 8 * g;
+      float* orow = (float*)(pbase + wave * wbytes) + rho * DP + 8 * g;
       // o[st][2b + par][e] holds dim 32b + 8g + 2e + par: dims 32b + 8g + 4h .. +3 are
       // (e, par) = (2h, 0), (2h, 1), (2h + 1, 0), (2h + 1, 1)
 #pragma unroll
       for (int b = 0; b < NB; b++)
 #pragma unroll
         for (int h = 0; h < 2; h++)
-          *(float4*)(orow + 32 * b + 4 * h) = make_float4(o[st][2 * b][2 * h] * f, o[st][2 * b + 1][2 * h] * f,
-                                                          o[st][2 * b][2 * h + 1] * f, o[st][2 * b + 1][2 * h + 1] * f);
+          *(float4*)(orow + 32 * b + 4 * h) = make_float4(o[st][2 * b][2 * h], o[st][2 * b + 1][2 * h],
+                                                          o[st][2 * b][2 * h + 1], o[st][2 * b + 1][2 * h + 1]);
     }
   }
   __syncthreads();
@@ -742,17 +727,24 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     const int c = tid + j * NTHR;
     if (c < C4) {
       const int rho = c / (D / 4), d = 4 * (c % (D / 4));
-      float4 acc = *(const float4*)(ow + (size_t)rho * DP + d);
-      float lt = lw[rho], mx = s_mw[0][rho];
+      float4 v[NW];
+      float mw[NW], mx = -INFINITY;
 #pragma unroll
-      for (int w = 1; w < NW; w++) {
-        const float4 v = *(const float4*)(ow + ((size_t)w * p.R + rho) * DP + d);
-        acc.x += v.x;
-        acc.y += v.y;
-        acc.z += v.z;
-        acc.w += v.w;
-        lt += lw[w * p.R + rho];
-        mx = fmaxf(mx, s_mw[w][rho]);
+      for (int w = 0; w < NW; w++) {
+        v[w] = *(const float4*)((const float*)(pbase + w * wbytes) + rho * DP + d);
+        mw[w] = s_mw[w][rho];
+        mx = fmaxf(mx, mw[w]);
+      }
+      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+      float lt = 0.0f;
+#pragma unroll
+      for (int w = 0; w < NW; w++) {
+        const float f = __builtin_amdgcn_exp2f(mw[w] - mx);
+        acc.x += v[w].x * f;
+        acc.y += v[w].y * f;
+        acc.z += v[w].z * f;
+        acc.w += v[w].w * f;
+        lt += s_lw[w][rho] * f;
       }
       if (single) {
         const int s = rho / p.G, h = kvh * p.G + rho % p.G;
@@ -954,21 +946,21 @@ static int rows_per_pass(int R) { return R > 4 ? 8 : 4; }
 static size_t decode_lds_bytes(int D, int dtype, int R, int NW, int PR) {
   const int nset = nset_for(R);
   const int RS = 16 * nset, NT = D / 32, NBV = dtype == KV_Q8 ? D / 32 : 1;
-  const size_t a = (size_t)((R + PR - 1) / PR) * NT * 2 * 64 * 16 + 32 + (size_t)NW * ((size_t)NBV * RS * 32 * 2 + (size_t)RS * 4);
-  const size_t b = (size_t)NW * R * (D + 5) * 4;
-  return a > b ? a : b;
+  const size_t t = (size_t)NBV * RS * 32 * 2 + (size_t)RS * 4, o = (size_t)R * (D + 4) * 4;
+  return (size_t)((R + PR - 1) / PR) * NT * 2 * 64 * 16 + 32 + (size_t)NW * (t > o ? t : o);
 }
-constexpr size_t kDecodeLdsMax = 159 * 1024;  // + the static wave maxima and ticket flag
+constexpr size_t kDecodeLdsMax = 158 * 1024;  // + the static wave maxima and sums (at most 1.5 KB)
 
 bool decode_supported(const LayerView& L, int S, int H) {
   if (L.dtype == KV_F32) return false;
   if (L.D != 128 && L.D != 256) return false;
   const int G = H / L.kv_heads;
   const int R = G * S;
-  // more rows than the operand and P^T tiles fit in LDS (D=256: about 20, counted with passes of
-  // 4 rows) go to the prefill kernel
+  // up to 48 rows at D=128 and 20 at D=256 (past that the D=256 row sets no longer fit the
+  // register file), within LDS; more go to the prefill kernel
   const int nw_max = (L.D == 128 && nset_for(R) == 1) ? 8 : 4;
-  return R >= 1 && nset_for(R) <= 3 && decode_lds_bytes(L.D, L.dtype, R, nw_max, 4) <= kDecodeLdsMax;
+  return R >= 1 && nset_for(R) <= 3 && (L.D == 128 || R <= 20) &&
+         decode_lds_bytes(L.D, L.dtype, R, nw_max, rows_per_pass(R)) <= kDecodeLdsMax;
 }
 
 bool decode_preferred(const LayerView& L, int S, int H) {

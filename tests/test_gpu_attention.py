@@ -128,8 +128,8 @@ def test_verify_rows_causal(dev, dtype, S):
 @pytest.mark.parametrize("dtype", ["f16", "q8"])
 @pytest.mark.parametrize("S", [2, 3, 4, 8])
 def test_verify_rows_hybrid_shape(dev, dtype, S):
-    """Qwen3.5 (24 heads on 4 kv heads, D=256) speculative verify: 6*S rows per kv head. The
-    decode kernel's LDS plan holds up to 18 q8 rows; more go to the prefill kernel."""
+    """Qwen3.5 (24 heads on 4 kv heads, D=256) speculative verify: 6*S rows per kv head. Up to
+    16 rows (one row set) run the decode kernel; more go to the prefill kernel."""
     out, exp = _raw_case(dtype, 24, 4, 256, 900 + S, S, seed=200 + S, gate=True, scale=1.0 / 16)
     _check(dtype, out, exp)
 
