@@ -37,6 +37,7 @@
 #include <algorithm>
 #include <map>
 #include <mutex>
+#include <type_traits>
 #include <utility>
 #include <vector>
 
@@ -148,8 +149,8 @@ constexpr int kUnitF4 = 17;  // float4 per (unit, split) slot
 // splits per kv head at most (the merge holds a column of every split in registers)
 constexpr int kMaxSplits = 256;
 
-// Shared memory plan (bytes): Q operands, per-wave P^T tiles, per-wave corr; after the tile
-// loop the same space holds the per-wave partials, then the split merge's weights and sums.
+// Shared memory plan (bytes): Q operands, then one part per wave: its P^T tiles and corr in the
+// tile loop, its raw partial o rows after it.
 template <int D, int DT, bool ROLL, int NSET, int NW, int PR>
 struct DecodeSmem {
   static constexpr bool QUARTER = (DT == KV_Q8) && !ROLL;
@@ -777,161 +778,194 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
   if (single || split < first_merger) return;
 
   // ---------------- merge (the last n_mergers splits) ----------------
-  // A merger polls its unit's slots of every split until none holds kPartialEmpty (the data
-  // itself is the completion signal: no flag, ticket or store acknowledgement to wait for), merges
-  // them by log-sum-exp, stores the output, and writes kPartialEmpty back for the next launch.
+  // Merger j (split first_merger + j) takes units j, j + n_mergers, .. (unit = one row x 64
+  // dims). The unit's slots of every split are polled until none holds kPartialEmpty (the data
+  // itself is the completion signal: no flag, ticket or store acknowledgement to wait for),
+  // merged by log-sum-exp, the output stored and kPartialEmpty written back for the next launch.
   // Mergers are the highest split indices, so workgroups are dispatched before the mergers that
   // wait on them; the host also sizes the grid to fit the GPU at once. The wait is bounded
   // (p.spin_limit rounds): a merger that gives up stores NaN and raises p.err.
-  // Thread (k, c) holds float4 column c of splits k, k + KG, .. (MAXL at a time); every wave
-  // also holds (m, l) of every split, one per lane, and derives the log-sum-exp maximum, sum and
-  // weights itself (the same DPP reductions in every wave, so the weights agree bit for bit):
-  // a thread takes its splits' weights from their lanes by ds_bpermute instead of from LDS
-  // behind a barrier. The empty markers go back as each batch is consumed, with the split in
-  // the scalar offset so that consecutive stores share their address registers (a register
-  // rewritten under a pending store makes the compiler wait for that store's acknowledgement).
-  constexpr int KG = NTHR / 16;                // split groups
-  // o slots per thread and batch (KG * MAXL splits a batch: 64 on 4 waves); 5 for the D=256
-  // one-tile kernel (4 waves, 80 a batch), whose 8193-8448-slot contexts (257-264 tiles) take
-  // 65-66 splits a kv head: one poll round instead of two (C5 decode 17.6 -> 16.95 us; 5 slots
-  // cost the D=128 one-tile kernel 0.1 us at 4k)
-  constexpr int MAXL = (ONE && D == 256) ? 5 : 4;
-  constexpr int MLC = (kMaxSplits + 63) / 64;  // (m, l) slots per lane of wave 0
-  const int c = tid & 15, k = tid >> 4;
-  float4* red = (float4*)smem;                                 // [NW][16]
+  // Up to 32 splits one wave merges a unit alone: no barrier and no LDS, so a unit is done as
+  // soon as its own slots have arrived (C3 32k 18.65 -> 17.8 us, C4 verify5 18.4 -> 17.0); when
+  // units outnumber the mergers, wave w of merger j takes units j + w * n_mergers, ... More
+  // splits (C5 decode: 65) are shared by the workgroup's waves (one wave polling 17 slots a lane
+  // a round measured 1.2 us slower), which meet once, at the sum of their parts.
+  // Lane (k, c) of split group kg holds float4 column c of splits kg, kg + KG, .. (OB at a time)
+  // and every lane l the (m, l) of splits l, l + 64, ..; the lane reductions give every wave the
+  // log-sum-exp maximum and sum (the same in every wave, bit for bit), and a lane takes its
+  // splits' weights from their lanes by ds_bpermute. The empty markers go back as each batch is
+  // consumed, with the split in the scalar offset so that consecutive stores share their address
+  // registers (a register rewritten under a pending store makes the compiler wait for that
+  // store's acknowledgement).
+  constexpr int MLC = (kMaxSplits + 63) / 64;  // (m, l) slots per lane
+  const int c = lane & 15, k = lane >> 4;
   const u32x4v empty4 = {kPartialEmpty, kPartialEmpty, kPartialEmpty, kPartialEmpty};
-  bool gave_up = false;  // wave-uniform; workgroup-uniform after each unit's reduction vote
-  for (int u = split - first_merger; u < units; u += p.n_mergers) {
-    const int rho = u / UPR, d0 = (u % UPR) * 64;
-    const int ubase = u * NS * kUnitF4;
-    floatx4 v[MAXL];
-    float2 ml[MLC];
-    // poll batch b0 of the o slots (wave 0 also the (m, l) slots) until nothing is missing;
-    // bounded: every split of the grid runs to completion on its own, so the data arrives, and
-    // the bound only guarantees an exit. Returns false when the bound ran out.
-    auto poll = [&](int b0, bool with_ml) -> bool {
-      for (int it = 0; it < p.spin_limit; it++) {
-        bool missing = false;
+  bool gave_up = false;  // wave-uniform
+  auto merge = [&](auto wg_tag) {
+    constexpr bool WG = decltype(wg_tag)::value;
+    constexpr int KG = WG ? 4 * NW : 4;  // split groups
+    // o slots per lane and batch: 8 for one wave (32 splits); across the workgroup 4, or 5 for
+    // the D=256 one-tile kernel (80 a batch: its 8193-8448-slot contexts take 65-66 splits)
+    constexpr int OB = WG ? ((ONE && D == 256) ? 5 : 4) : 8;
+    const int kg = WG ? 4 * wave + k : k;
+    const int j0 = split - first_merger;
+    for (int u = WG ? j0 : j0 + wave * p.n_mergers; u < units; u += WG ? p.n_mergers : p.n_mergers * NW) {
+      const int rho = u / UPR, d0 = (u % UPR) * 64;
+      const int ubase = u * NS * kUnitF4;
+      floatx4 v[OB];
+      float2 ml[MLC];
+      // poll batch b0 of the o slots (and the (m, l) slots) until nothing is missing; bounded:
+      // every split of the grid runs to completion on its own, so the data arrives, and the
+      // bound only guarantees an exit. Returns false when the bound ran out.
+      auto poll = [&](int b0, bool with_ml) -> bool {
+        for (int it = 0; it < p.spin_limit; it++) {
+          bool missing = false;
 #pragma unroll
-        for (int i = 0; i < MAXL; i++) {
-          const int sp = b0 + k + KG * i;
-          v[i] = sp < NS ? __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(wrs, (ubase + sp * kUnitF4 + c) * 16, 0, kSC1))
-                         : floatx4{0.f, 0.f, 0.f, 0.f};
+          for (int i = 0; i < OB; i++) {
+            const int sp = b0 + kg + KG * i;
+            v[i] = sp < NS ? __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(wrs, (ubase + sp * kUnitF4 + c) * 16, 0, kSC1))
+                           : floatx4{0.f, 0.f, 0.f, 0.f};
+          }
+          if (with_ml) {
+#pragma unroll
+            for (int j = 0; j < MLC; j++) {
+              const int sp = 64 * j + lane;
+              ml[j] = make_float2(-INFINITY, 0.0f);
+              if (64 * j < NS && sp < NS)
+                ml[j] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(wrs, (ubase + sp * kUnitF4 + 16) * 16, 0, kSC1));
+            }
+#pragma unroll
+            for (int j = 0; j < MLC; j++)
+              missing = missing || __float_as_uint(ml[j].x) == kPartialEmpty || __float_as_uint(ml[j].y) == kPartialEmpty;
+          }
+#pragma unroll
+          for (int i = 0; i < OB; i++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) missing = missing || __float_as_uint(v[i][e]) == kPartialEmpty;
+          if (!__any(missing)) return true;
+          __builtin_amdgcn_s_sleep(1);
         }
-        if (with_ml) {
+        return false;
+      };
+      // the weights of every split: w[j] at lane l is split 64 j + l
+      float w[MLC];
+      // consume a batch: weighted sum, then mark its slots empty again
+      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+      const int vo = (ubase + kg * kUnitF4 + c) * 16;
+      auto consume = [&](int b0) {
+#pragma unroll
+        for (int i = 0; i < OB; i++) {
+          const int sp = b0 + kg + KG * i;
+          // the weight of split sp from lane sp % 64 of w[sp / 64]
+          float wi = 0.0f;
 #pragma unroll
           for (int j = 0; j < MLC; j++) {
-            const int sp = 64 * j + lane;
-            ml[j] = make_float2(-INFINITY, 0.0f);
-            if (64 * j < NS && sp < NS)
-              ml[j] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(wrs, (ubase + sp * kUnitF4 + 16) * 16, 0, kSC1));
+            if (64 * j < NS) {
+              const float t = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * (sp & 63), __float_as_int(w[j])));
+              wi = (sp >> 6) == j ? t : wi;
+            }
           }
-#pragma unroll
-          for (int j = 0; j < MLC; j++)
-            missing = missing || __float_as_uint(ml[j].x) == kPartialEmpty || __float_as_uint(ml[j].y) == kPartialEmpty;
-        }
-#pragma unroll
-        for (int i = 0; i < MAXL; i++)
-#pragma unroll
-          for (int e = 0; e < 4; e++) missing = missing || __float_as_uint(v[i][e]) == kPartialEmpty;
-        // a vote of this wave only: every wave holds every (m, l) and polls its own o slots,
-        // so the waves meet once, at the reduction below
-        if (!__any(missing)) return true;
-        __builtin_amdgcn_s_sleep(1);
-      }
-      return false;
-    };
-    // the weights of every split, one per lane of every wave: w[j] at lane l is split 64 j + l
-    float w[MLC];
-    // consume a batch: weighted sum, then mark its slots empty again
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    const int vo = (ubase + k * kUnitF4 + c) * 16;
-    auto consume = [&](int b0) {
-#pragma unroll
-      for (int i = 0; i < MAXL; i++) {
-        const int sp = b0 + k + KG * i;
-        // the weight of split sp from lane sp % 64 of w[sp / 64]
-        float wi = 0.0f;
-#pragma unroll
-        for (int j = 0; j < MLC; j++) {
-          if (64 * j < NS) {
-            const float t = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * (sp & 63), __float_as_int(w[j])));
-            wi = (sp >> 6) == j ? t : wi;
+          if (sp < NS) {
+            acc.x += v[i][0] * wi;
+            acc.y += v[i][1] * wi;
+            acc.z += v[i][2] * wi;
+            acc.w += v[i][3] * wi;
+            __builtin_amdgcn_raw_buffer_store_b128(empty4, wrs, vo, (b0 + KG * i) * kUnitF4 * 16, kSC1);
           }
         }
-        if (sp < NS) {
-          acc.x += v[i][0] * wi;
-          acc.y += v[i][1] * wi;
-          acc.z += v[i][2] * wi;
-          acc.w += v[i][3] * wi;
-          __builtin_amdgcn_raw_buffer_store_b128(empty4, wrs, vo, (b0 + KG * i) * kUnitF4 * 16, kSC1);
+      };
+      gave_up = !poll(0, true) || gave_up;
+      {
+        float M = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < MLC; j++) M = fmaxf(M, ml[j].x);
+        M = wave_max(M);
+        float lt = 0.0f;
+#pragma unroll
+        for (int j = 0; j < MLC; j++) lt += ml[j].y * __builtin_amdgcn_exp2f(ml[j].x - M);
+        lt = wave_sum(lt);
+#pragma unroll
+        for (int j = 0; j < MLC; j++) w[j] = __builtin_amdgcn_exp2f(ml[j].x - M) / lt;
+      }
+      // the (m, l) slots back to empty once every wave that reads them has (one wave: now;
+      // the workgroup: wave 0 after the waves meet below)
+      auto reset_ml = [&]() {
+        const int vm = (ubase + lane * kUnitF4 + 16) * 16;
+#pragma unroll
+        for (int j = 0; j < MLC; j++)
+          if (64 * j + lane < NS) __builtin_amdgcn_raw_buffer_store_b128(empty4, wrs, vm, 64 * j * kUnitF4 * 16, kSC1);
+      };
+      if constexpr (!WG) reset_ml();
+      consume(0);
+      for (int b0 = KG * OB; b0 < NS; b0 += KG * OB) {
+        gave_up = !poll(b0, false) || gave_up;
+        consume(b0);
+      }
+      // the four split groups of a wave hold the same column in lanes c, c + 16, c + 32, c + 48:
+      // two permlane swaps sum them
+      {
+        float* a4 = &acc.x;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          float2 t = pair16(a4[e]);
+          a4[e] = t.x + t.y;
+          t = pair32(a4[e]);
+          a4[e] = t.x + t.y;
         }
       }
-    };
-    gave_up = !poll(0, true) || gave_up;
-    {
-      float M = -INFINITY;
+      if constexpr (WG) {
+        // the waves' parts meet in LDS (the operand space: the wave combine above no longer
+        // reads it), one barrier; wave 0 sums them
+        float4* red = (float4*)smem;  // [NW][16]
+        int* gu = (int*)(red + NW * 16);
+        if (lane < 16) red[wave * 16 + c] = acc;
+        if (lane == 0) gu[wave] = gave_up;
+        __syncthreads();
+        if (wave == 0) {
+          reset_ml();
+          float4 part[NW];
+          int g2 = 0;
 #pragma unroll
-      for (int j = 0; j < MLC; j++) M = fmaxf(M, ml[j].x);
-      M = wave_max(M);
-      float lt = 0.0f;
+          for (int w2 = 0; w2 < NW; w2++) {
+            part[w2] = red[w2 * 16 + c];
+            g2 |= gu[w2];
+          }
+          acc = part[0];
 #pragma unroll
-      for (int j = 0; j < MLC; j++) lt += ml[j].y * __builtin_amdgcn_exp2f(ml[j].x - M);
-      lt = wave_sum(lt);
+          for (int w2 = 1; w2 < NW; w2++) {
+            acc.x += part[w2].x;
+            acc.y += part[w2].y;
+            acc.z += part[w2].z;
+            acc.w += part[w2].w;
+          }
+          gave_up = g2 != 0;
+        }
+      }
+      if ((!WG || wave == 0) && lane < 16) {
+        const int s = rho / p.G, h = kvh * p.G + rho % p.G, d = d0 + 4 * c;
+        float r[4] = {acc.x, acc.y, acc.z, acc.w};
+        if (p.gate) {
+          const float* gr = p.gate + ((size_t)s * p.H + h) * p.gate_stride + d;
 #pragma unroll
-      for (int j = 0; j < MLC; j++) w[j] = __builtin_amdgcn_exp2f(ml[j].x - M) / lt;
-    }
-    consume(0);
-    for (int b0 = KG * MAXL; b0 < NS; b0 += KG * MAXL) {
-      gave_up = !poll(b0, false) || gave_up;
-      consume(b0);
-    }
-    // the four split groups of a wave hold the same column in lanes l, l^16, l^32, l^48: two
-    // permlane swaps sum them, then the waves' sums go through LDS
-    {
-      float* a4 = &acc.x;
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        float2 t = pair16(a4[e]);
-        a4[e] = t.x + t.y;
-        t = pair32(a4[e]);
-        a4[e] = t.x + t.y;
+          for (int e = 0; e < 4; e++) r[e] = r[e] / (1.0f + expf(-gr[e]));
+        }
+        if (gave_up) r[0] = r[1] = r[2] = r[3] = __builtin_nanf("");
+        *(float4*)(p.out + ((size_t)s * p.H + h) * D + d) = make_float4(r[0], r[1], r[2], r[3]);
+      }
+      // the next unit's parts reuse the LDS space
+      if constexpr (WG) {
+        if (u + p.n_mergers < units) __syncthreads();
       }
     }
-    if (lane < 16) red[wave * 16 + c] = acc;
-    gave_up = __syncthreads_or(gave_up);
-    // every wave has read every (m, l): wave 0 marks those slots empty again
-    if (wave == 0) {
-      const int vm = (ubase + lane * kUnitF4 + 16) * 16;
-#pragma unroll
-      for (int j = 0; j < MLC; j++)
-        if (64 * j + lane < NS) __builtin_amdgcn_raw_buffer_store_b128(empty4, wrs, vm, 64 * j * kUnitF4 * 16, kSC1);
-    }
-    if (tid < 16) {
-#pragma unroll
-      for (int w = 1; w < NW; w++) {
-        const float4 w4 = red[w * 16 + c];
-        acc.x += w4.x;
-        acc.y += w4.y;
-        acc.z += w4.z;
-        acc.w += w4.w;
-      }
-      const int s = rho / p.G, h = kvh * p.G + rho % p.G, d = d0 + 4 * c;
-      float r[4] = {acc.x, acc.y, acc.z, acc.w};
-      if (p.gate) {
-        const float* gr = p.gate + ((size_t)s * p.H + h) * p.gate_stride + d;
-#pragma unroll
-        for (int e = 0; e < 4; e++) r[e] = r[e] / (1.0f + expf(-gr[e]));
-      }
-      if (gave_up) r[0] = r[1] = r[2] = r[3] = __builtin_nanf("");
-      *(float4*)(p.out + ((size_t)s * p.H + h) * D + d) = make_float4(r[0], r[1], r[2], r[3]);
-    }
-    __syncthreads();
-  }
+  };
+  if (NS > 32)
+    merge(std::true_type{});
+  else
+    merge(std::false_type{});
   // one vector store from one lane, system scope: the host reads the word without a copy. 2:
   // the L2 exchange was on, so a split may have stored on another XCD (the library then writes
   // partials through); a split withheld by the test hook is no placement question (1)
-  if (gave_up && tid == 0)
+  if (gave_up && lane == 0)
     __hip_atomic_store(p.err, (p.xcd_local > 0 && p.withhold_split < 0) ? 2u : 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
@@ -940,7 +974,7 @@ static int nset_for(int R) { return (R + 15) / 16; }
 static int rows_per_pass(int R) { return R > 4 ? 8 : 4; }
 
 // dynamic LDS of the tile loop and wave combine (DecodeSmem::total for the launch's template
-// arguments); the split merge needs less (weights and 16 float4 per split group)
+// arguments); the split merge uses none
 // NW: waves per workgroup (the most a shape launches with, 8 for D=128 single-set, bounds the rest);
 // PR: query rows per pass
 static size_t decode_lds_bytes(int D, int dtype, int R, int NW, int PR) {
@@ -1013,7 +1047,8 @@ bool decode_plan(const LayerView& L, int S, int H, int pos_base, int num_cus, in
   }
   s.tiles_per_split = tps;
   s.n_splits = ns;
-  const int units = R * (L.D / 64);  // merge units: one row x 64 dims
+  // merge units (one row x 64 dims), one a merging split
+  const int units = R * (L.D / 64);
   s.n_mergers = ns > 1 ? (units < ns ? units : ns) : 0;
   s.grid = ns * L.kv_heads;
   s.xcd_group = 0;
@@ -1114,11 +1149,8 @@ static hipError_t launch_cfg(const LayerView& L, const AttnArgs& a, hipStream_t 
   const int R = (a.H / L.kv_heads) * a.S;
   if (rows_per_pass(R) != PR) return hipErrorInvalidValue;
   const int NP = (R + PR - 1) / PR;
-  size_t smem = SM::total(NP, R);
+  const size_t smem = SM::total(NP, R);
   if (smem != decode_lds_bytes(D, DT, R, NW, PR)) return hipErrorInvalidValue;  // the two plans agree
-  // the merge reuses the space ([waves][16] float4; the bound keeps an older, larger plan)
-  const size_t merge_max = (((size_t)kMaxSplits * 4 + 15) & ~(size_t)15) + (size_t)NW * 16 * 16;
-  smem = smem > merge_max ? smem : merge_max;
   if (smem > kDecodeLdsMax) return hipErrorInvalidValue;
   {
     std::lock_guard<std::mutex> lock(g_decode_fn_mu);
@@ -1185,7 +1217,7 @@ static hipError_t launch_nset(const LayerView& L, const AttnArgs& a, int nset, h
       // two-tile kernel's prefetch would re-read the wave's only tile)
       if constexpr (DT == KV_Q8) {
         auto one_tile = [&](const void* fn, int pr) {
-          const size_t smem = std::max(decode_lds_bytes(D, DT, R, 4, pr), (((size_t)kMaxSplits * 4 + 15) & ~(size_t)15) + 4 * 16 * 16);
+          const size_t smem = decode_lds_bytes(D, DT, R, 4, pr);
           DecodePlan p1;
           return decode_plan(L, a.S, a.H, a.pos_base, a.num_cus, resident_blocks(fn, 256, smem), &p1) &&
                  p1.waves == 4 && (p1.n_splits > 1 ? p1.tiles_per_split == 4 : p1.n_tiles <= 4);
