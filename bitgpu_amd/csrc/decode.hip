@@ -808,12 +808,14 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     // the D=256 one-tile kernel (80 a batch: its 8193-8448-slot contexts take 65-66 splits)
     constexpr int OB = WG ? ((ONE && D == 256) ? 5 : 4) : 8;
     const int kg = WG ? 4 * wave + k : k;
+    // (m, l) registers per lane: one covers the 32 splits a wave merges alone
+    constexpr int MLU = WG ? MLC : 1;
     const int j0 = split - first_merger;
     for (int u = WG ? j0 : j0 + wave * p.n_mergers; u < units; u += WG ? p.n_mergers : p.n_mergers * NW) {
       const int rho = u / UPR, d0 = (u % UPR) * 64;
       const int ubase = u * NS * kUnitF4;
       floatx4 v[OB];
-      float2 ml[MLC];
+      float2 ml[MLU];
       // poll batch b0 of the o slots (and the (m, l) slots) until nothing is missing; bounded:
       // every split of the grid runs to completion on its own, so the data arrives, and the
       // bound only guarantees an exit. Returns false when the bound ran out.
@@ -828,14 +830,14 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
           }
           if (with_ml) {
 #pragma unroll
-            for (int j = 0; j < MLC; j++) {
+            for (int j = 0; j < MLU; j++) {
               const int sp = 64 * j + lane;
               ml[j] = make_float2(-INFINITY, 0.0f);
               if (64 * j < NS && sp < NS)
                 ml[j] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(wrs, (ubase + sp * kUnitF4 + 16) * 16, 0, kSC1));
             }
 #pragma unroll
-            for (int j = 0; j < MLC; j++)
+            for (int j = 0; j < MLU; j++)
               missing = missing || __float_as_uint(ml[j].x) == kPartialEmpty || __float_as_uint(ml[j].y) == kPartialEmpty;
           }
 #pragma unroll
@@ -847,52 +849,58 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
         }
         return false;
       };
-      // the weights of every split: w[j] at lane l is split 64 j + l
-      float w[MLC];
-      // consume a batch: weighted sum, then mark its slots empty again
+      // the weights of every split: w[j] at lane l is split 64 j + l (0 past the last split)
+      float w[MLU];
+      // consume a batch: weighted sum, then mark its slots empty again. Every weight is fetched
+      // before any is used (one LDS wait), and slots past the last split hold zeros.
       float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
       const int vo = (ubase + kg * kUnitF4 + c) * 16;
       auto consume = [&](int b0) {
+        float wi[OB];
 #pragma unroll
         for (int i = 0; i < OB; i++) {
           const int sp = b0 + kg + KG * i;
           // the weight of split sp from lane sp % 64 of w[sp / 64]
-          float wi = 0.0f;
+          wi[i] = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * (sp & 63), __float_as_int(w[0])));
 #pragma unroll
-          for (int j = 0; j < MLC; j++) {
-            if (64 * j < NS) {
-              const float t = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * (sp & 63), __float_as_int(w[j])));
-              wi = (sp >> 6) == j ? t : wi;
-            }
-          }
-          if (sp < NS) {
-            acc.x += v[i][0] * wi;
-            acc.y += v[i][1] * wi;
-            acc.z += v[i][2] * wi;
-            acc.w += v[i][3] * wi;
-            __builtin_amdgcn_raw_buffer_store_b128(empty4, wrs, vo, (b0 + KG * i) * kUnitF4 * 16, kSC1);
+          for (int j = 1; j < MLU; j++) {
+            const float t = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * (sp & 63), __float_as_int(w[j])));
+            wi[i] = (sp >> 6) == j ? t : wi[i];
           }
         }
+#pragma unroll
+        for (int i = 0; i < OB; i++) {
+          acc.x += v[i][0] * wi[i];
+          acc.y += v[i][1] * wi[i];
+          acc.z += v[i][2] * wi[i];
+          acc.w += v[i][3] * wi[i];
+        }
+#pragma unroll
+        for (int i = 0; i < OB; i++)
+          if (b0 + kg + KG * i < NS) __builtin_amdgcn_raw_buffer_store_b128(empty4, wrs, vo, (b0 + KG * i) * kUnitF4 * 16, kSC1);
       };
       gave_up = !poll(0, true) || gave_up;
       {
         float M = -INFINITY;
 #pragma unroll
-        for (int j = 0; j < MLC; j++) M = fmaxf(M, ml[j].x);
+        for (int j = 0; j < MLU; j++) M = fmaxf(M, ml[j].x);
         M = wave_max(M);
-        float lt = 0.0f;
+        float e[MLU], lt = 0.0f;
 #pragma unroll
-        for (int j = 0; j < MLC; j++) lt += ml[j].y * __builtin_amdgcn_exp2f(ml[j].x - M);
-        lt = wave_sum(lt);
+        for (int j = 0; j < MLU; j++) {
+          e[j] = __builtin_amdgcn_exp2f(ml[j].x - M);
+          lt += ml[j].y * e[j];
+        }
+        const float rl = 1.0f / wave_sum(lt);
 #pragma unroll
-        for (int j = 0; j < MLC; j++) w[j] = __builtin_amdgcn_exp2f(ml[j].x - M) / lt;
+        for (int j = 0; j < MLU; j++) w[j] = e[j] * rl;
       }
       // the (m, l) slots back to empty once every wave that reads them has (one wave: now;
       // the workgroup: wave 0 after the waves meet below)
       auto reset_ml = [&]() {
         const int vm = (ubase + lane * kUnitF4 + 16) * 16;
 #pragma unroll
-        for (int j = 0; j < MLC; j++)
+        for (int j = 0; j < MLU; j++)
           if (64 * j + lane < NS) __builtin_amdgcn_raw_buffer_store_b128(empty4, wrs, vm, 64 * j * kUnitF4 * 16, kSC1);
       };
       if constexpr (!WG) reset_ml();
