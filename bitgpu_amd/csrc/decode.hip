@@ -845,6 +845,9 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
       // bound only guarantees an exit. Returns false when the bound ran out.
       auto poll = [&](int b0, bool with_ml) -> bool {
         for (int it = 0; it < p.spin_limit; it++) {
+          // a compiler memory barrier: every round's loads are issued again (other workgroups
+          // write the slots; without it the compiler may reuse the last round's values)
+          __asm__ volatile("" ::: "memory");
           bool missing = false;
 #pragma unroll
           for (int i = 0; i < OB; i++) {
@@ -903,7 +906,56 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
         for (int i = 0; i < OB; i++)
           if (b0 + kg + KG * i < NS) __builtin_amdgcn_raw_buffer_store_b128(empty4, wrs, vo, (b0 + KG * i) * kUnitF4 * 16, kSC1);
       };
-      gave_up = !poll(0, true) || gave_up;
+      if constexpr (WG) {
+        gave_up = !poll(0, true) || gave_up;
+      } else {
+        // one wave, every split in one batch: two poll rounds in flight, each check waits only
+        // for the older round, so a slot that lands is seen about half a round trip sooner.
+        // The loads are unconditional (slots past the last split re-read the last split's, and
+        // are zeroed once complete), so the wait can count the younger round's loads.
+        auto issue = [&](floatx4 (&vv)[OB], float2 (&mm)[MLU]) {
+          __asm__ volatile("" ::: "memory");  // issued again every round (see poll)
+#pragma unroll
+          for (int i = 0; i < OB; i++) {
+            const int sp = min(kg + KG * i, NS - 1);
+            vv[i] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(wrs, (ubase + sp * kUnitF4 + c) * 16, 0, kSC1));
+          }
+          mm[0] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(wrs, (ubase + min(lane, NS - 1) * kUnitF4 + 16) * 16, 0, kSC1));
+          __builtin_amdgcn_sched_barrier(0);  // the round is issued before the older one is checked
+        };
+        auto complete = [&](const floatx4 (&vv)[OB], const float2 (&mm)[MLU]) {
+          bool missing = __float_as_uint(mm[0].x) == kPartialEmpty || __float_as_uint(mm[0].y) == kPartialEmpty;
+#pragma unroll
+          for (int i = 0; i < OB; i++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) missing = missing || __float_as_uint(vv[i][e]) == kPartialEmpty;
+          return !__any(missing);
+        };
+        floatx4 v2[OB];
+        float2 ml2[MLU];
+        bool ok = false;
+        issue(v, ml);
+        for (int it = 0; it < p.spin_limit; it++) {
+          issue(v2, ml2);
+          if (complete(v, ml)) {
+            ok = true;
+            break;
+          }
+          issue(v, ml);
+          if (complete(v2, ml2)) {
+#pragma unroll
+            for (int i = 0; i < OB; i++) v[i] = v2[i];
+            ml[0] = ml2[0];
+            ok = true;
+            break;
+          }
+        }
+        gave_up = !ok || gave_up;
+#pragma unroll
+        for (int i = 0; i < OB; i++)
+          if (kg + KG * i >= NS) v[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+        if (lane >= NS) ml[0] = make_float2(-INFINITY, 0.0f);
+      }
       {
         float M = -INFINITY;
 #pragma unroll
