@@ -398,6 +398,9 @@ __global__ __launch_bounds__(kQkvThreads) void qkv_proj_kernel(LayerView L, QkvP
     const int spins = a.spin_limit > 0 ? a.spin_limit : (1 << 20);
     bool missing = true;
     for (int it = 0; it < spins && missing; it++) {
+      // a compiler memory barrier: the load is issued again every round (other workgroups
+      // write the rows; without it the compiler may reuse the last round's value)
+      __asm__ volatile("" ::: "memory");
       const floatx4_t v = __builtin_bit_cast(floatx4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, 16 * c, 0, kSC1));
 #pragma unroll
       for (int e = 0; e < 4; e++) x[e] = v[e];
