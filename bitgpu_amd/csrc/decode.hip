@@ -315,7 +315,10 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
   const float* ksb = p.L.ks + (size_t)kvh * cap * NB;
   const float* vsb = p.L.vs + (size_t)kvh * cap * NB;
 
-  const int t_begin = split * p.tiles_per_split;
+  // splits take the tiles in reverse order: the last, shorter range goes to split 0 (dispatched
+  // first), the mergers (the highest splits) take the first tiles (C4 verify5 16.89 -> 16.44 us,
+  // C4 decode 11.31 -> 11.13, C5 decode 14.75 -> 14.52)
+  const int t_begin = (p.n_splits - 1 - split) * p.tiles_per_split;
   const int t_end = min(t_begin + p.tiles_per_split, p.n_tiles);
 
   // Q operands (block diagonal, hi/lo f16). The setup is straight-line code -- every load is
