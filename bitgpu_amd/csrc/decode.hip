@@ -317,7 +317,8 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
 
   // splits take the tiles in reverse order: the last, shorter range goes to split 0 (dispatched
   // first), the mergers (the highest splits) take the first tiles (C4 verify5 16.89 -> 16.44 us,
-  // C4 decode 11.31 -> 11.13, C5 decode 14.75 -> 14.52)
+  // C4 decode 11.31 -> 11.13, C5 decode 14.75 -> 14.52; the plain order measured 0.7-0.85 us
+  // slower for the one-tile kernel at 2049-8192 slots and C3 4k)
   const int t_begin = (p.n_splits - 1 - split) * p.tiles_per_split;
   const int t_end = min(t_begin + p.tiles_per_split, p.n_tiles);
 
@@ -353,7 +354,11 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     __builtin_amdgcn_s_waitcnt(0xf70);  // vmcnt(0): q has arrived
     __builtin_amdgcn_sched_barrier(0);
     const int ta = tile0 < t_end ? tile0 : t_end - 1;
-    load_tile<D, DT, QUARTER, PR>(A, ta * 32, g, n, kbase, vbase, ksb, vsb);
+    // one-tile kernel: a wave without a tile (the short last range) still issues its loads, but
+    // every lane at the same address, so that they fetch next to nothing (C5 decode at 8193
+    // slots: 65 splits, 260 workgroups, four CUs hold two)
+    const bool own = !ONE || tile0 < t_end;
+    load_tile<D, DT, QUARTER, PR>(A, ta * 32, own ? g : 0, own ? n : 0, kbase, vbase, ksb, vsb);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < QMAX; i++) {
