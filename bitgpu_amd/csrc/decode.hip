@@ -354,10 +354,11 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     __builtin_amdgcn_s_waitcnt(0xf70);  // vmcnt(0): q has arrived
     __builtin_amdgcn_sched_barrier(0);
     const int ta = tile0 < t_end ? tile0 : t_end - 1;
-    // one-tile kernel: a wave without a tile (the short last range) still issues its loads, but
-    // every lane at the same address, so that they fetch next to nothing (C5 decode at 8193
-    // slots: 65 splits, 260 workgroups, four CUs hold two)
-    const bool own = !ONE || tile0 < t_end;
+    // a wave without a tile (the short last range) still issues its loads, but every lane at
+    // the same address, so that they fetch next to nothing (C5 decode at 8193 slots: 65 splits,
+    // 260 workgroups, four CUs hold two; 14.42 -> 12.92 us); the same for every load of a tile
+    // the wave does not own below
+    const bool own = tile0 < t_end;
     load_tile<D, DT, QUARTER, PR>(A, ta * 32, own ? g : 0, own ? n : 0, kbase, vbase, ksb, vsb);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -633,7 +634,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
   } else if constexpr (DT == KV_Q8) {
     {
       const int tb = nmy > 1 ? tile0 + NW : (tile0 < t_end ? tile0 : t_end - 1);
-      load_tile<D, DT, QUARTER, PR>(B, tb * 32, g, n, kbase, vbase, ksb, vsb);
+      load_tile<D, DT, QUARTER, PR>(B, tb * 32, nmy > 1 ? g : 0, nmy > 1 ? n : 0, kbase, vbase, ksb, vsb);
     }
     for (; it + 4 <= nmy; it += 2) {
       const int ta = tile0 + it * NW;
@@ -665,14 +666,15 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
   } else {
     // f16 tiles are twice as large: the registers hold two whole tiles, so the next tile is
     // issued before a tile is processed and re-issued only after both of its phases (past the
-    // end the prefetch re-reads the tile just loaded, still cached)
+    // end the prefetch is issued at one address)
     for (; it + 2 <= nmy; it += 2) {
       const int ta = tile0 + it * NW;
       load_tile<D, DT, QUARTER, PR>(B, (ta + NW) * 32, g, n, kbase, vbase, ksb, vsb);
       qk_softmax(A, ta);
       pv(A);
-      const int tn = it + 2 < nmy ? ta + 2 * NW : ta + NW;
-      load_tile<D, DT, QUARTER, PR>(A, tn * 32, g, n, kbase, vbase, ksb, vsb);
+      const bool next = it + 2 < nmy;
+      const int tn = next ? ta + 2 * NW : ta + NW;
+      load_tile<D, DT, QUARTER, PR>(A, tn * 32, next ? g : 0, next ? n : 0, kbase, vbase, ksb, vsb);
       qk_softmax(B, ta + NW);
       pv(B);
     }
