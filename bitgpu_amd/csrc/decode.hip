@@ -848,6 +848,14 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     for (int u = WG ? j0 : j0 + wave * p.n_mergers; u < units; u += WG ? p.n_mergers : p.n_mergers * NW) {
       const int rho = u / UPR, d0 = (u % UPR) * 64;
       const int ubase = u * NS * kUnitF4;
+      // the gate's sigmoid denominators (gate_sigmoid.wgsl: x / (1 + exp(-g))) before the wait,
+      // so that its load is not a memory round trip after the merge
+      float gden[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+      if (p.gate) {
+        const float* gr = p.gate + ((size_t)(rho / p.G) * p.H + kvh * p.G + rho % p.G) * p.gate_stride + d0 + 4 * c;
+#pragma unroll
+        for (int e = 0; e < 4; e++) gden[e] = 1.0f + expf(-gr[e]);
+      }
       floatx4 v[OB];
       float2 ml[MLU];
       // poll batch b0 of the o slots (and the (m, l) slots) until nothing is missing; bounded:
@@ -1039,9 +1047,8 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
         const int s = rho / p.G, h = kvh * p.G + rho % p.G, d = d0 + 4 * c;
         float r[4] = {acc.x, acc.y, acc.z, acc.w};
         if (p.gate) {
-          const float* gr = p.gate + ((size_t)s * p.H + h) * p.gate_stride + d;
 #pragma unroll
-          for (int e = 0; e < 4; e++) r[e] = r[e] / (1.0f + expf(-gr[e]));
+          for (int e = 0; e < 4; e++) r[e] = r[e] / gden[e];
         }
         if (gave_up) r[0] = r[1] = r[2] = r[3] = __builtin_nanf("");
         *(float4*)(p.out + ((size_t)s * p.H + h) * D + d) = make_float4(r[0], r[1], r[2], r[3]);
