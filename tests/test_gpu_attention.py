@@ -144,12 +144,15 @@ def test_decode_gate_hybrid_shape(dev):
 # kv head merge one (row, 64-dim) unit each (one wave alone up to 32 splits). Shapes: (24,4,256) L=4097 -> 52 splits, 24 units;
 # (16,2,128) L=32768 -> 128 splits (one poll batch of 128); (2,2,128) -> 128 splits of one row;
 # (4,1,256) L=32768 -> 256 splits, polled in batches; (16,1,256) L=5120 -> 40 splits for 64
-# units (the workgroup-wide merge, two units a merger); (32,8,128) S=12 -> 48 rows per kv head
-# (past one 16-row set: the split-K prefill kernel and its merge).
+# units (the workgroup-wide merge, two units a merger); (24,1,128) L=1024 q8 -> 8 splits for 48
+# units on 32 merging waves (the one-wave merge, two units a wave; f16 runs the prefill kernel);
+# (32,8,128) S=12 -> 48 rows per kv head (past one 16-row set: the split-K prefill kernel and its
+# merge).
 @pytest.mark.parametrize("dtype", ["f16", "q8"])
 @pytest.mark.parametrize("H,KV,D,L,S,gate", [(24, 4, 256, 4097, 1, True), (16, 2, 128, 32768, 1, False),
                                              (2, 2, 128, 32768, 1, False), (4, 1, 256, 32768, 1, False),
-                                             (16, 1, 256, 5120, 1, True), (32, 8, 128, 4108, 12, False)])
+                                             (16, 1, 256, 5120, 1, True), (24, 1, 128, 1024, 1, True),
+                                             (32, 8, 128, 4108, 12, False)])
 def test_decode_merge_paths(dev, dtype, H, KV, D, L, S, gate):
     out, exp = _raw_case(dtype, H, KV, D, L, S, seed=L + H, gate=gate)
     _check(dtype, out, exp)

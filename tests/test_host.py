@@ -205,7 +205,7 @@ _DECODE_SHAPES = [(8, 128, 1, 32, L) for L in (1, 31, 32, 33, 517, 4096, 4097, 1
     (4, 256, 1, 24, 4097), (2, 128, 1, 16, 32768), (2, 128, 1, 2, 32768), (1, 256, 1, 4, 32768),
     (8, 128, 12, 32, 4108), (8, 128, 5, 32, 4000), (8, 128, 5, 32, 3749), (4, 256, 2, 24, 902), (4, 256, 3, 24, 903),
     (4, 256, 1, 24, 8193), (3, 128, 1, 12, 32768), (5, 128, 1, 20, 20000), (8, 128, 1, 32, 3745),
-    (1, 256, 1, 16, 5120)]
+    (1, 256, 1, 16, 5120), (1, 128, 1, 24, 1024)]
 
 
 @pytest.mark.parametrize("KV,D,S,H,L", _DECODE_SHAPES)
