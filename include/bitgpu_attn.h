@@ -237,7 +237,8 @@ int32_t bg_qkv_proj_prologue(bg_kv_cache* cache, int32_t layer, const float* x, 
  * 1/sqrt(head_dim), attention_sg.wgsl:24; the hybrid passes 1/sqrt(head_dim) as a param).
  * gate (nullable): [S, H, gate_stride], out = attn / (1 + exp(-gate)) (gate_sigmoid.wgsl:13).
  * out: [S, H, head_dim] f32. Rows per kv head (S x H / KV) that fit one 16-row set run the
- * split-K decode kernel (and so does sink mode up to 48 rows, and q8 at head_dim 128 up to 24);
+ * split-K decode kernel (and so does sink mode up to 48 rows at head_dim 128 and 20 at 256, and
+ * q8 at head_dim 128 up to 24);
  * more run the MFMA prefill kernel, whose grid is split along the key range (a second kernel
  * merging the parts) when it holds far fewer query blocks than the GPU has CUs; f32 storage runs
  * an exact-f32 kernel. */
