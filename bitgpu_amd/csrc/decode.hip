@@ -252,12 +252,43 @@ __device__ __forceinline__ void load_tile_v(TileRegs<D, DT, QUARTER, PR>& T, int
   }
 }
 
-template <int D, int DT, bool QUARTER, int PR>
-__device__ __forceinline__ void load_tile(TileRegs<D, DT, QUARTER, PR>& T, int j0, int g, int n,
-                                          const unsigned char* kbase, const unsigned char* vbase,
-                                          const float* ksb, const float* vsb) {
-  load_tile_k<D, DT, QUARTER, PR>(T, j0, g, n, kbase, ksb, vsb);
-  load_tile_v<D, DT, QUARTER, PR>(T, j0, g, n, vbase);
+// Sink mode: the rope rows of a tile's two slots a lane rotates (cos and sin of its lane group's
+// D/8 dims of the first half, at each slot's rope position), loaded with the tile's K part so
+// that the rotation does not wait a memory round trip after the tile has arrived. ON = false (no
+// rotation, or a kernel without the registers for it): empty, and the rotation reads the table
+// itself.
+template <int D, bool ON>
+struct RopeRegs {
+  float4 c[2][D / 32], s[2][D / 32];
+};
+template <int D>
+struct RopeRegs<D, false> {};
+
+// the table row of physical slot P (sink-mode positions: logical slot, plus the evicted count past
+// the sinks in absolute mode; slots past the ring and rows past the table read row 0, unused)
+__device__ __forceinline__ long rope_row(const LayerView& L, int phys_limit, int P) {
+  int Lg = L.ring.logical(P);
+  Lg = P < phys_limit ? Lg : 0;
+  long ri = (L.rope_abs && Lg >= L.ring.sinks) ? (long)Lg + L.evicted : (long)Lg;
+  return ri < L.rope_positions ? ri : 0;
+}
+
+template <int D, bool ON>
+__device__ __forceinline__ void load_rope(RopeRegs<D, ON>& R, const LayerView& L, int phys_limit, int j0, int g,
+                                          int n) {
+  if constexpr (ON) {
+#pragma unroll
+    for (int t2 = 0; t2 < 2; t2++) {
+      const long ri = rope_row(L, phys_limit, j0 + 16 * t2 + n);
+      const float* ct = L.cos_tab + (size_t)ri * (D / 2) + g * (D / 8);
+      const float* st = L.sin_tab + (size_t)ri * (D / 2) + g * (D / 8);
+#pragma unroll
+      for (int i = 0; i < D / 32; i++) {
+        R.c[t2][i] = *(const float4*)(ct + 4 * i);
+        R.s[t2][i] = *(const float4*)(st + 4 * i);
+      }
+    }
+  }
 }
 
 // PR: query rows per QK pass (4, or 8 for more than 4 rows: half the MFMAs, operand reads and
@@ -326,6 +357,12 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
   // unconditional (spare slots read query 0, a wave without tiles re-reads the split's last
   // tile) and spare slots store to a sink.
   TR A, B;
+  // sink mode at D = 128 on 4-wave workgroups of up to two row sets: each tile's rope rows travel
+  // with its K part (the 64 registers a tile more would spill the 8-wave kernels, whose waves have
+  // half the register file, and the three-set one)
+  constexpr bool RPRE = ROLL && D == 128 && NW == 4 && NSET <= 2;
+  using RP = RopeRegs<D, RPRE>;
+  RP RA, RB;
   const int tile0 = t_begin + wave;
   {
     constexpr int QMAX = (NPK * NT * 64 + NTHR - 1) / NTHR;  // operand slots per thread
@@ -359,7 +396,9 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     // 260 workgroups, four CUs hold two; 14.42 -> 12.92 us); the same for every load of a tile
     // the wave does not own below
     const bool own = tile0 < t_end;
-    load_tile<D, DT, QUARTER, PR>(A, ta * 32, own ? g : 0, own ? n : 0, kbase, vbase, ksb, vsb);
+    load_tile_k<D, DT, QUARTER, PR>(A, ta * 32, own ? g : 0, own ? n : 0, kbase, ksb, vsb);
+    load_rope<D, RPRE>(RA, p.L, p.phys_limit, ta * 32, own ? g : 0, own ? n : 0);
+    load_tile_v<D, DT, QUARTER, PR>(A, ta * 32, own ? g : 0, own ? n : 0, vbase);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < QMAX; i++) {
@@ -399,7 +438,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     for (int i = 0; i < D / 16; i++) o[s][i] = floatx4{0, 0, 0, 0};
 
   bool rescale = false;  // the last qk_softmax raised a reference max: pv rescales O first
-  auto qk_softmax = [&](const TR& T, int tile) {
+  auto qk_softmax = [&](const TR& T, const RP& Rr, int tile) {
     const int j0 = tile * 32;
     // ---------------- K operands ----------------
     // K operand for QK MFMA t of 16-slot group t2: converted just in time (plain cache) or
@@ -423,11 +462,8 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
         (void)t2;
       } else {
         // read-time rotation: dims (i, i + D/2) of this lane group, at the slot's rope position
-        const int P = j0 + 16 * t2 + n;
-        int Lg = ring.logical(P);
-        Lg = P < p.phys_limit ? Lg : 0;
-        long ri = (p.L.rope_abs && Lg >= ring.sinks) ? (long)Lg + p.L.evicted : (long)Lg;
-        ri = ri < p.L.rope_positions ? ri : 0;
+        // (the rows in Rr, or read here without the prefetch)
+        const long ri = RPRE ? 0 : rope_row(p.L, p.phys_limit, j0 + 16 * t2 + n);
         const float* ct = p.L.cos_tab + (size_t)ri * (D / 2) + g * (D / 8);
         const float* st = p.L.sin_tab + (size_t)ri * (D / 2) + g * (D / 8);
         constexpr int HT = NT / 2;  // MFMAs per half
@@ -456,7 +492,15 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
           H8 r0, r1;
 #pragma unroll
           for (int e = 0; e < 8; e++) {
-            const float c = ct[8 * t + e], s = st[8 * t + e];
+            float c, s;
+            if constexpr (RPRE) {
+              const float4 cv = Rr.c[t2][2 * t + e / 4], sv = Rr.s[t2][2 * t + e / 4];
+              c = (e & 3) == 0 ? cv.x : (e & 3) == 1 ? cv.y : (e & 3) == 2 ? cv.z : cv.w;
+              s = (e & 3) == 0 ? sv.x : (e & 3) == 1 ? sv.y : (e & 3) == 2 ? sv.z : sv.w;
+            } else {
+              c = ct[8 * t + e];
+              s = st[8 * t + e];
+            }
             r0.h[e] = (_Float16)__fadd_rn(__fmul_rn(a[e], c), __fmul_rn(-b2[e], s));
             r1.h[e] = (_Float16)__fadd_rn(__fmul_rn(b2[e], c), __fmul_rn(a[e], s));
           }
@@ -624,43 +668,55 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
   // and there is no early exit, so every path into a loop head has the same loads outstanding
   // and the compiler counts them instead of draining them.
   const int nmy = tile0 < t_end ? (t_end - tile0 + NW - 1) / NW : 0;  // this wave's tiles
+  // a tile's K part (with its rope rows) and its V part
+  auto issue_k = [&](TR& T, RP& Rr, int tile, int gg, int nn) {
+    load_tile_k<D, DT, QUARTER, PR>(T, tile * 32, gg, nn, kbase, ksb, vsb);
+    load_rope<D, RPRE>(Rr, p.L, p.phys_limit, tile * 32, gg, nn);
+  };
+  auto issue_v = [&](TR& T, int tile, int gg, int nn) {
+    load_tile_v<D, DT, QUARTER, PR>(T, tile * 32, gg, nn, vbase);
+  };
   int it = 0;
   if constexpr (ONE) {
     (void)it;
     if (nmy >= 1) {
-      qk_softmax(A, tile0);
+      qk_softmax(A, RA, tile0);
       pv(A);
     }
   } else if constexpr (DT == KV_Q8) {
     {
       const int tb = nmy > 1 ? tile0 + NW : (tile0 < t_end ? tile0 : t_end - 1);
-      load_tile<D, DT, QUARTER, PR>(B, tb * 32, nmy > 1 ? g : 0, nmy > 1 ? n : 0, kbase, vbase, ksb, vsb);
+      issue_k(B, RB, tb, nmy > 1 ? g : 0, nmy > 1 ? n : 0);
+      issue_v(B, tb, nmy > 1 ? g : 0, nmy > 1 ? n : 0);
     }
     for (; it + 4 <= nmy; it += 2) {
       const int ta = tile0 + it * NW;
-      qk_softmax(A, ta);
-      load_tile_k<D, DT, QUARTER, PR>(A, (ta + 2 * NW) * 32, g, n, kbase, ksb, vsb);
+      qk_softmax(A, RA, ta);
+      issue_k(A, RA, ta + 2 * NW, g, n);
       pv(A);
-      load_tile_v<D, DT, QUARTER, PR>(A, (ta + 2 * NW) * 32, g, n, vbase);
-      qk_softmax(B, ta + NW);
-      load_tile_k<D, DT, QUARTER, PR>(B, (ta + 3 * NW) * 32, g, n, kbase, ksb, vsb);
+      issue_v(A, ta + 2 * NW, g, n);
+      qk_softmax(B, RB, ta + NW);
+      issue_k(B, RB, ta + 3 * NW, g, n);
       pv(B);
-      load_tile_v<D, DT, QUARTER, PR>(B, (ta + 3 * NW) * 32, g, n, vbase);
+      issue_v(B, ta + 3 * NW, g, n);
     }
     // the last one to three tiles: A and B hold tiles it and it + 1
     const int r = nmy - it;
     const int ta = tile0 + it * NW;
     if (r >= 1) {
-      qk_softmax(A, ta);
+      qk_softmax(A, RA, ta);
       pv(A);
     }
-    if (r == 3) load_tile<D, DT, QUARTER, PR>(A, (ta + 2 * NW) * 32, g, n, kbase, vbase, ksb, vsb);
+    if (r == 3) {
+      issue_k(A, RA, ta + 2 * NW, g, n);
+      issue_v(A, ta + 2 * NW, g, n);
+    }
     if (r >= 2) {
-      qk_softmax(B, ta + NW);
+      qk_softmax(B, RB, ta + NW);
       pv(B);
     }
     if (r == 3) {
-      qk_softmax(A, ta + 2 * NW);
+      qk_softmax(A, RA, ta + 2 * NW);
       pv(A);
     }
   } else {
@@ -669,17 +725,19 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     // end the prefetch is issued at one address)
     for (; it + 2 <= nmy; it += 2) {
       const int ta = tile0 + it * NW;
-      load_tile<D, DT, QUARTER, PR>(B, (ta + NW) * 32, g, n, kbase, vbase, ksb, vsb);
-      qk_softmax(A, ta);
+      issue_k(B, RB, ta + NW, g, n);
+      issue_v(B, ta + NW, g, n);
+      qk_softmax(A, RA, ta);
       pv(A);
       const bool next = it + 2 < nmy;
       const int tn = next ? ta + 2 * NW : ta + NW;
-      load_tile<D, DT, QUARTER, PR>(A, tn * 32, next ? g : 0, next ? n : 0, kbase, vbase, ksb, vsb);
-      qk_softmax(B, ta + NW);
+      issue_k(A, RA, tn, next ? g : 0, next ? n : 0);
+      issue_v(A, tn, next ? g : 0, next ? n : 0);
+      qk_softmax(B, RB, ta + NW);
       pv(B);
     }
     if (it < nmy) {
-      qk_softmax(A, tile0 + it * NW);
+      qk_softmax(A, RA, tile0 + it * NW);
       pv(A);
     }
   }
