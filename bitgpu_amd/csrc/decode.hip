@@ -501,8 +501,12 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
               c = ct[8 * t + e];
               s = st[8 * t + e];
             }
-            r0.h[e] = (_Float16)__fadd_rn(__fmul_rn(a[e], c), __fmul_rn(-b2[e], s));
-            r1.h[e] = (_Float16)__fadd_rn(__fmul_rn(b2[e], c), __fmul_rn(a[e], s));
+            // the products with s as fma(x, s, +0) (the same value as x * s but for the sign of
+            // a zero, which the sum below cannot see): the f16 x then enters a mixed-precision
+            // fma directly instead of being converted first
+            const float bs = __builtin_fmaf(b2[e], s, 0.0f), as = __builtin_fmaf(a[e], s, 0.0f);
+            r0.h[e] = (_Float16)__fadd_rn(__fmul_rn(a[e], c), -bs);
+            r1.h[e] = (_Float16)__fadd_rn(__fmul_rn(b2[e], c), as);
           }
           kb[t2][t] = r0.h;
           kb[t2][HT + t] = r1.h;
