@@ -49,6 +49,7 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4v __attribute__((ext_vector_type(4)));
+typedef int i32x4v __attribute__((ext_vector_type(4)));
 typedef unsigned u32x2v __attribute__((ext_vector_type(2)));
 
 constexpr int NW = 4;  // waves per workgroup
@@ -305,10 +306,13 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
   constexpr int NBV = SM::NBV;
   constexpr int RS = SM::RS;
   constexpr int NB = D / 32;         // q8 scale blocks per row
-  constexpr int NSUB = QUARTER ? TR::KSN : 1;  // scale blocks a lane's output rows see
   constexpr int KU = TR::KU;
   constexpr int RL = PR / 4;         // query rows per lane and pass after the reduction
   constexpr int NTHR = 64 * NW;
+  // q8 without rotation: QK on the int8 matrix cores (the K codes as they are)
+  constexpr bool I8 = QUARTER;
+  constexpr int NT8 = D / 64;        // int8 QK MFMAs per 16-slot group (16 dims a lane group each)
+  constexpr int NSB = TR::KSN;       // scale blocks a lane's output rows see
 
   extern __shared__ __align__(16) unsigned char smem[];
   const int tid = threadIdx.x;
@@ -364,7 +368,91 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
   using RP = RopeRegs<D, RPRE>;
   RP RA, RB;
   const int tile0 = t_begin + wave;
-  {
+  // The first tile is issued once q has arrived (q issued alone returns in ~0.3 us, while
+  // behind every CU's first tile, ~19 MB queued at once, it returns only after them), and the
+  // query's conversion below runs while the tile streams in. The scheduling barriers keep the
+  // compiler from moving the tile loads above the wait or below the conversion.
+  auto issue_first = [&]() {
+    __builtin_amdgcn_s_waitcnt(0xf70);  // vmcnt(0): q has arrived
+    __builtin_amdgcn_sched_barrier(0);
+    const int ta = tile0 < t_end ? tile0 : t_end - 1;
+    // a wave without a tile (the short last range) still issues its loads, but every lane at
+    // the same address, so that they fetch next to nothing (C5 decode at 8193 slots: 65 splits,
+    // 260 workgroups, four CUs hold two; 14.42 -> 12.92 us); the same for every load of a tile
+    // the wave does not own below
+    const bool own = tile0 < t_end;
+    load_tile_k<D, DT, QUARTER, PR>(A, ta * 32, own ? g : 0, own ? n : 0, kbase, ksb, vsb);
+    load_rope<D, RPRE>(RA, p.L, p.phys_limit, ta * 32, own ? g : 0, own ? n : 0);
+    load_tile_v<D, DT, QUARTER, PR>(A, ta * 32, own ? g : 0, own ? n : 0, vbase);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  if constexpr (I8) {
+    // int8 operands: lane (gg, ii) of pass `pass` holds, for each int8 MFMA t8, the 16 dims
+    // qk_dim(gg, 2 t8, 0..15) of A row ii's query (zero off the block diagonal) as hi and lo
+    // bytes, value ~ scale * (hi + lo / 256) with the scale = max |value| of the row's 32-dim
+    // scale block / 127. A thread takes one float4 of one (pass, A row, block): the 8 threads
+    // of a block are neighbouring lanes, which share its max by three swaps, and each writes its
+    // 4 dims' bytes into the lane and MFMA that hold them (PR = 4: lane group ii / 4, MFMA
+    // 2 b + c / 4; PR = 8: lane group 2 (ii / 8) + c / 4, MFMA b).
+    constexpr int QI = (NPK * 16 * NSB * 8 + NTHR - 1) / NTHR;  // float4 chunks per thread
+    const int NQC = NP * 16 * NSB * 8;
+    float4 qv[QI];
+#pragma unroll
+    for (int i = 0; i < QI; i++) {
+      const int u = i * NTHR + tid;
+      const int c = u & 7, unit = u >> 3;
+      const int b = unit % NSB, ii = (unit / NSB) & 15, pass = unit / (16 * NSB);
+      const int rho = PR * pass + (ii & (PR - 1));
+      const bool use = u < NQC && rho < p.R;
+      const int s = use ? rho / p.G : 0, h = use ? kvh * p.G + rho % p.G : 0;
+      const int d = PR == 4 ? (ii >> 2) * (D / 4) + 32 * b + 4 * c : (ii >> 3) * (D / 2) + 32 * b + 4 * c;
+      qv[i] = *(const float4*)(p.q + ((size_t)s * p.H + h) * D + (use ? d : 0));
+      if (!use) qv[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    issue_first();
+    unsigned char* q8b = (unsigned char*)smem;                      // [NP][NT8][hi, lo][64] x 16 bytes
+    float* qsc = (float*)(q8b + (size_t)NP * NT8 * 2 * 64 * 16);  // [NP][NSB][16 A rows]
+#pragma unroll
+    for (int i = 0; i < QI; i++) {
+      const int u = i * NTHR + tid;
+      const int c = u & 7, unit = u >> 3;
+      const int b = unit % NSB, ii = (unit / NSB) & 15, pass = unit / (16 * NSB);
+      float4 f = qv[i];
+      f.x *= p.qscale;
+      f.y *= p.qscale;
+      f.z *= p.qscale;
+      f.w *= p.qscale;
+      float mx = fmaxf(fmaxf(fabsf(f.x), fabsf(f.y)), fmaxf(fabsf(f.z), fabsf(f.w)));
+      mx = fmaxf(mx, __shfl_xor(mx, 1));
+      mx = fmaxf(mx, __shfl_xor(mx, 2));
+      mx = fmaxf(mx, __shfl_xor(mx, 4));
+      if (u < NQC) {
+        const float inv = mx > 0.0f ? 127.0f / mx : 0.0f;
+        const float y[4] = {f.x * inv, f.y * inv, f.z * inv, f.w * inv};
+        uint32_t hv = 0, lv = 0;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const float hf = rintf(y[e]);
+          const float lf = fminf(fmaxf(rintf((y[e] - hf) * 256.0f), -127.0f), 127.0f);
+          hv |= ((uint32_t)(int)hf & 255u) << (8 * e);
+          lv |= ((uint32_t)(int)lf & 255u) << (8 * e);
+        }
+        const int gg = PR == 4 ? ii >> 2 : 2 * (ii >> 3) + (c >> 2);
+        const int t8 = PR == 4 ? 2 * b + (c >> 2) : b;
+        const int l = 16 * gg + ii;
+        uint32_t* o = (uint32_t*)(q8b + ((size_t)((pass * NT8 + t8) * 2) * 64 + l) * 16) + (c & 3);
+        o[0] = hv;        // hi
+        o[64 * 4] = lv;   // lo: the next 64 lanes' slots
+        if (c == 0) qsc[(pass * NSB + b) * 16 + ii] = mx * (1.0f / (127.0f * 256.0f));
+      }
+    }
+    // the off-diagonal operand slots are zero
+    for (int i = tid; i < NP * NT8 * 2 * 64; i += NTHR) {
+      const int l = i & 63, gg = l >> 4, ii = l & 15;
+      const bool diag = PR == 4 ? (ii >> 2) == gg : (ii >> 3) == (gg >> 1);
+      if (!diag) *(uint4*)(q8b + (size_t)i * 16) = make_uint4(0, 0, 0, 0);
+    }
+  } else {
     constexpr int QMAX = (NPK * NT * 64 + NTHR - 1) / NTHR;  // operand slots per thread
     const int NQ = NP * NT * 64;
     float qv[QMAX][8];
@@ -384,22 +472,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
       qv[i][0] = a.x; qv[i][1] = a.y; qv[i][2] = a.z; qv[i][3] = a.w;
       qv[i][4] = b.x; qv[i][5] = b.y; qv[i][6] = b.z; qv[i][7] = b.w;
     }
-    // The first tile is issued once q has arrived (q issued alone returns in ~0.3 us, while
-    // behind every CU's first tile, ~19 MB queued at once, it returns only after them), and the
-    // hi/lo conversion below runs while the tile streams in. The scheduling barriers keep the
-    // compiler from moving the tile loads above the wait or below the conversion.
-    __builtin_amdgcn_s_waitcnt(0xf70);  // vmcnt(0): q has arrived
-    __builtin_amdgcn_sched_barrier(0);
-    const int ta = tile0 < t_end ? tile0 : t_end - 1;
-    // a wave without a tile (the short last range) still issues its loads, but every lane at
-    // the same address, so that they fetch next to nothing (C5 decode at 8193 slots: 65 splits,
-    // 260 workgroups, four CUs hold two; 14.42 -> 12.92 us); the same for every load of a tile
-    // the wave does not own below
-    const bool own = tile0 < t_end;
-    load_tile_k<D, DT, QUARTER, PR>(A, ta * 32, own ? g : 0, own ? n : 0, kbase, ksb, vsb);
-    load_rope<D, RPRE>(RA, p.L, p.phys_limit, ta * 32, own ? g : 0, own ? n : 0);
-    load_tile_v<D, DT, QUARTER, PR>(A, ta * 32, own ? g : 0, own ? n : 0, vbase);
-    __builtin_amdgcn_sched_barrier(0);
+    issue_first();
 #pragma unroll
     for (int i = 0; i < QMAX; i++) {
       const int idx = i * NTHR + tid;
@@ -441,15 +514,13 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
   auto qk_softmax = [&](const TR& T, const RP& Rr, int tile) {
     const int j0 = tile * 32;
     // ---------------- K operands ----------------
-    // K operand for QK MFMA t of 16-slot group t2: converted just in time (plain cache) or
-    // materialized once after the read-time rotation (sink mode)
+    // f16 K operand for QK MFMA t of 16-slot group t2: as loaded (f16 cache) or materialized
+    // once after the read-time rotation (sink mode); q8 codes without rotation enter the int8
+    // MFMAs as they are
     half8 kb[2][ROLL ? NT : 1];
     auto kop = [&](int t2, int t) -> half8 {
       if constexpr (ROLL) {
         return kb[t2][t];
-      } else if constexpr (DT == KV_Q8) {
-        const uint4 u = T.kr[t2][t >> 1];
-        return (t & 1) ? q8_to_half8(u.z, u.w) : q8_to_half8(u.x, u.y);
       } else {
         H8 h;  // piece 0 holds MFMAs t < NT/2, piece 1 the rest, stored back to back
         h.u = T.kr[t2][t];
@@ -522,32 +593,55 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     for (int pass = 0; pass < NPK; pass++) {
       if (pass >= NP) break;
       float sc[2][RL];
+      // int8: the query scales of the lane's C rows 4g .. 4g+3, one float4 a block
+      float4 qsv[I8 ? NSB : 1];
+      if constexpr (I8) {
+        const float* qsc = (const float*)((const unsigned char*)smem + (size_t)NP * NT8 * 2 * 64 * 16);
+#pragma unroll
+        for (int b = 0; b < NSB; b++) qsv[b] = *(const float4*)(qsc + (pass * NSB + b) * 16 + 4 * g);
+      }
 #pragma unroll
       for (int t2 = 0; t2 < 2; t2++) {
-        floatx4 c[NSUB];
-#pragma unroll
-        for (int i = 0; i < NSUB; i++) c[i] = floatx4{0, 0, 0, 0};
-#pragma unroll
-        for (int t = 0; t < NT; t++) {
-          H8 ahi, alo;
-          ahi.u = qs[((pass * NT + t) * 2 + 0) * 64 + lane];
-          alo.u = qs[((pass * NT + t) * 2 + 1) * 64 + lane];
-          const int sub = QUARTER ? (PR == 4 ? t >> 2 : t >> 1) : 0;
-          const half8 kt = kop(t2, t);
-          c[sub] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi.h, kt, c[sub], 0, 0, 0);
-          c[sub] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo.h, kt, c[sub], 0, 0, 0);
-        }
         float v[4];
+        if constexpr (I8) {
+          // C row 4g+e of block b: the integer sum of hi x code plus that of lo x code / 256,
+          // exact in int32 (|sum| <= 32 * 127 * 127 a block), times the query and key scales
+          const u32x4v* q8o = (const u32x4v*)smem;
+          i32x4v ch[NSB], cl[NSB];
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-          if constexpr (QUARTER) {
-            float acc = c[0][e] * T.ksc[t2][0];
+          for (int b = 0; b < NSB; b++) ch[b] = cl[b] = i32x4v{0, 0, 0, 0};
 #pragma unroll
-            for (int i = 1; i < NSUB; i++) acc = fmaf(c[i][e], T.ksc[t2][i], acc);
-            v[e] = acc;
-          } else {
-            v[e] = c[0][e];
+          for (int t8 = 0; t8 < NT8; t8++) {
+            const int b = PR == 4 ? t8 >> 1 : t8;
+            const i32x4v ahi = __builtin_bit_cast(i32x4v, q8o[((pass * NT8 + t8) * 2 + 0) * 64 + lane]);
+            const i32x4v alo = __builtin_bit_cast(i32x4v, q8o[((pass * NT8 + t8) * 2 + 1) * 64 + lane]);
+            const i32x4v kt = __builtin_bit_cast(i32x4v, T.kr[t2][t8]);
+            ch[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi, kt, ch[b], 0, 0, 0);
+            cl[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo, kt, cl[b], 0, 0, 0);
           }
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int b = 0; b < NSB; b++) {
+              const float qk = (e == 0 ? qsv[b].x : e == 1 ? qsv[b].y : e == 2 ? qsv[b].z : qsv[b].w) * T.ksc[t2][b];
+              acc = fmaf((float)(ch[b][e] * 256 + cl[b][e]), qk, acc);
+            }
+            v[e] = acc;
+          }
+        } else {
+          floatx4 c = floatx4{0, 0, 0, 0};
+#pragma unroll
+          for (int t = 0; t < NT; t++) {
+            H8 ahi, alo;
+            ahi.u = qs[((pass * NT + t) * 2 + 0) * 64 + lane];
+            alo.u = qs[((pass * NT + t) * 2 + 1) * 64 + lane];
+            const half8 kt = kop(t2, t);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi.h, kt, c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo.h, kt, c, 0, 0, 0);
+          }
+#pragma unroll
+          for (int e = 0; e < 4; e++) v[e] = c[e];
         }
         // Lane group g' holds output rows 4g'..4g'+3 (v[0..3]) of the slot. permlane32_swap(a, b)
         // leaves lanes l < 32 with {a[l], a[l+32]} and lanes l >= 32 with {b[l-32], b[l]};
@@ -607,12 +701,15 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
         const int rho = row_of(pass, i);
         if (rescale) {
           const float mn = fmaxf(m[pass][i], mts[pass][i]);
-          const float corr = exp2f(m[pass][i] - mn);
+          // the hardware exp2 (no denormal results: a factor below 2^-126 becomes 0, which
+          // changes no f32 sum that also holds the tile's own terms >= 2^-8, nor an f16 P)
+          const float corr = __builtin_amdgcn_exp2f(m[pass][i] - mn);
           lsum[pass][i] *= corr;
           m[pass][i] = mn;
           if (n == 0 && rho < RS) cl[rho] = corr;
         }
-        const float p0 = exp2f(xs[pass][i][0] - m[pass][i]), p1 = exp2f(xs[pass][i][1] - m[pass][i]);
+        const float p0 = __builtin_amdgcn_exp2f(xs[pass][i][0] - m[pass][i]);
+        const float p1 = __builtin_amdgcn_exp2f(xs[pass][i][1] - m[pass][i]);
         lsum[pass][i] += p0 + p1;
         if (rho < RS) {
 #pragma unroll
