@@ -612,7 +612,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q8 KV (int8 codes + f32 scales), f16 MFMA operands, f32 accumulate",
+        "dtype": "q8 KV (int8 codes + f32 scales); QK on int8 MFMA (codes x hi/lo int8 query, int32 accumulate), PV on f16 MFMA (f32 accumulate)",
         "data": "synthetic (seeded N(0,1) K/V, RMSNorm+RoPE through the fused prologue)",
         "config": {"workload": "C3 decode attention, 36 distinct layers x 32768 cached positions, batch 1",
                    "heads": 32, "kv_heads": 8, "head_dim": 128, "kv_cache": "q8", "context": L, "layers": 36},

@@ -81,6 +81,19 @@ def test_c1_decode_f32_golden(dev):
     c.close()
 
 
+# ------------------------------------------------------------------ q8 int8 query error budget
+@pytest.mark.parametrize("H,KV,D,S", [(32, 8, 128, 1), (32, 8, 128, 2), (24, 4, 256, 1)])
+@pytest.mark.parametrize("sharp", [1.0, 8.0])
+def test_q8_decode_int8_query_error(dev, H, KV, D, S, sharp):
+    """q8 decode without rotation takes QK on the int8 matrix cores: the query enters as
+    hi + lo/256 int8 parts of its 32-dim blocks over the block max / 127 (representation error
+    at most 2^-9 / 127 of the block max). The output stays well inside the 2e-3 bar, also for
+    queries 8x sharper than unit variance (a numpy model of the split gives 3e-5 and 1.2e-4);
+    a lost lo part would give about 6e-3."""
+    out, exp = _raw_case("q8", H, KV, D, 4096, S, seed=31, scale=sharp / np.sqrt(D))
+    assert rel_err(out, exp) <= 5e-4, rel_err(out, exp)
+
+
 # ------------------------------------------------------------------ reference kernel case
 @pytest.mark.parametrize("dtype", ["f32", "f16", "q8"])
 def test_reference_kernel_case(dev, dtype):
