@@ -1288,11 +1288,12 @@ bool decode_plan(const LayerView& L, int S, int H, int pos_base, int num_cus, in
   const int tps_min = (s.n_tiles + kMaxSplits - 1) / kMaxSplits;
   tps = tps < tps_min ? tps_min : tps;
   const long resident = (long)(resident_per_cu > 0 ? resident_per_cu : 1) * cus;
-  // a q8 4-wave single-set plan whose waves would take two tiles at one workgroup a CU takes one
-  // tile a wave instead when a CU holds two workgroups and the GPU holds the larger grid (q8
-  // tiles cost more compute per byte, so two tiles in series on one wave cost more than a CU
-  // running two workgroups; measured slower for f16)
-  if (L.dtype == KV_Q8 && s.waves == 4 && s.nset == 1 && resident_per_cu >= 2 && tps > s.waves && tps <= 2 * s.waves) {
+  // a q8 or sink-mode 4-wave single-set plan whose waves would take two tiles at one workgroup a
+  // CU takes one tile a wave instead when a CU holds two workgroups and the GPU holds the larger
+  // grid (q8 and rotated tiles cost more compute per byte, so two tiles in series on one wave
+  // cost more than a CU running two workgroups: C4 decode 10.67 -> 10.23 us; measured slower for
+  // plain f16)
+  if ((L.dtype == KV_Q8 || L.ring.roll) && s.waves == 4 && s.nset == 1 && resident_per_cu >= 2 && tps > s.waves && tps <= 2 * s.waves) {
     const int ns1 = (s.n_tiles + s.waves - 1) / s.waves;
     if (ns1 <= kMaxSplits && (long)ns1 * L.kv_heads <= resident) tps = s.waves;
   }
@@ -1473,9 +1474,9 @@ static hipError_t launch_nset(const LayerView& L, const AttnArgs& a, int nset, h
           return launch_cfg<D, DT, ROLL, 1, 2, 8, 8>(L, a, st);
         }
       }
-      // q8: one tile a wave when the plan for the one-tile kernel's residency gives it (the
-      // two-tile kernel's prefetch would re-read the wave's only tile)
-      if constexpr (DT == KV_Q8) {
+      // q8 and sink mode: one tile a wave when the plan for the one-tile kernel's residency gives
+      // it (the two-tile kernel's prefetch would re-read the wave's only tile)
+      if constexpr (DT == KV_Q8 || ROLL) {
         auto one_tile = [&](const void* fn, int pr) {
           const size_t smem = decode_lds_bytes(D, DT, R, 4, pr);
           DecodePlan p1;
