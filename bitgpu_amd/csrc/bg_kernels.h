@@ -135,6 +135,7 @@ struct DecodePlan {
   int n_scan, phys_limit, n_tiles;
   int tiles_per_split, n_splits, n_mergers, grid;
   int xcd_group;  // > 0: splits numbered in groups of this many per kv head (sink mode), grid padded
+  int skip_t0, skip_n;  // a run of whole tiles every row masks (sink mode), not scanned
 };
 bool decode_plan(const LayerView& L, int S, int H, int pos_base, int num_cus, int resident_per_cu, DecodePlan* out);
 // streaming-read floor (diag.hip): `workgroups` contiguous slices of `bytes` read with 16-byte

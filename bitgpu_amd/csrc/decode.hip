@@ -121,6 +121,9 @@ struct DecodeParams {
   int n_scan;        // physical slots to scan
   int phys_limit;    // physical slots that can hold data
   int n_tiles, tiles_per_split, n_splits;
+  // tiles skip_t0 .. skip_t0 + skip_n - 1 hold only slots that every row masks (empty ring slots
+  // in sink mode) and are not scanned: tile index t covers slots from 32 (t < skip_t0 ? t : t + skip_n)
+  int skip_t0, skip_n;
   // split partials, [KV][units][n_splits][17] float4 with unit = (row, 64-dim chunk): 16 float4
   // of o, then (m, l, -, -). Every slot holds kPartialEmpty except between a split's store and
   // the merger's read of it in the same launch.
@@ -356,6 +359,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
   // slower for the one-tile kernel at 2049-8192 slots and C3 4k)
   const int t_begin = (p.n_splits - 1 - split) * p.tiles_per_split;
   const int t_end = min(t_begin + p.tiles_per_split, p.n_tiles);
+  auto sl = [&](int t) { return 32 * (t < p.skip_t0 ? t : t + p.skip_n); };  // first slot of tile t
 
   // Q operands (block diagonal, hi/lo f16). The setup is straight-line code -- every load is
   // unconditional (spare slots read query 0, a wave without tiles re-reads the split's last
@@ -381,9 +385,9 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     // 260 workgroups, four CUs hold two; 14.42 -> 12.92 us); the same for every load of a tile
     // the wave does not own below
     const bool own = tile0 < t_end;
-    load_tile_k<D, DT, QUARTER, PR>(A, ta * 32, own ? g : 0, own ? n : 0, kbase, ksb, vsb);
-    load_rope<D, RPRE>(RA, p.L, p.phys_limit, ta * 32, own ? g : 0, own ? n : 0);
-    load_tile_v<D, DT, QUARTER, PR>(A, ta * 32, own ? g : 0, own ? n : 0, vbase);
+    load_tile_k<D, DT, QUARTER, PR>(A, sl(ta), own ? g : 0, own ? n : 0, kbase, ksb, vsb);
+    load_rope<D, RPRE>(RA, p.L, p.phys_limit, sl(ta), own ? g : 0, own ? n : 0);
+    load_tile_v<D, DT, QUARTER, PR>(A, sl(ta), own ? g : 0, own ? n : 0, vbase);
     __builtin_amdgcn_sched_barrier(0);
   };
   if constexpr (I8) {
@@ -512,7 +516,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
 
   bool rescale = false;  // the last qk_softmax raised a reference max: pv rescales O first
   auto qk_softmax = [&](const TR& T, const RP& Rr, int tile) {
-    const int j0 = tile * 32;
+    const int j0 = sl(tile);
     // ---------------- K operands ----------------
     // f16 K operand for QK MFMA t of 16-slot group t2: as loaded (f16 cache) or materialized
     // once after the read-time rotation (sink mode); q8 codes without rotation enter the int8
@@ -771,11 +775,11 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
   const int nmy = tile0 < t_end ? (t_end - tile0 + NW - 1) / NW : 0;  // this wave's tiles
   // a tile's K part (with its rope rows) and its V part
   auto issue_k = [&](TR& T, RP& Rr, int tile, int gg, int nn) {
-    load_tile_k<D, DT, QUARTER, PR>(T, tile * 32, gg, nn, kbase, ksb, vsb);
-    load_rope<D, RPRE>(Rr, p.L, p.phys_limit, tile * 32, gg, nn);
+    load_tile_k<D, DT, QUARTER, PR>(T, sl(tile), gg, nn, kbase, ksb, vsb);
+    load_rope<D, RPRE>(Rr, p.L, p.phys_limit, sl(tile), gg, nn);
   };
   auto issue_v = [&](TR& T, int tile, int gg, int nn) {
-    load_tile_v<D, DT, QUARTER, PR>(T, tile * 32, gg, nn, vbase);
+    load_tile_v<D, DT, QUARTER, PR>(T, sl(tile), gg, nn, vbase);
   };
   int it = 0;
   if constexpr (ONE) {
@@ -1281,6 +1285,36 @@ bool decode_plan(const LayerView& L, int S, int H, int pos_base, int num_cus, in
   s.n_scan = (L.ring.roll && L.ring.head != 0) ? L.max_seq : pos_base + S;
   s.phys_limit = L.ring.roll ? L.max_seq : L.cap;
   s.n_tiles = (s.n_scan + 31) / 32;
+  // sink mode after the wrap scans every physical slot; the ring slots whose logical index lies
+  // past the last row's position (the room eviction left) are masked for every row, and the
+  // longest run of whole tiles of them is skipped (C4 at position 100000: 11 of 129 tiles)
+  s.skip_t0 = 0;
+  s.skip_n = 0;
+  if (L.ring.roll && L.ring.head != 0) {
+    const int sk = L.ring.sinks, W = L.ring.W;
+    const int first = pos_base + S;  // the first logical slot no row sees
+    if (first >= sk && first < sk + W) {
+      const int a = sk + (first - sk + L.ring.head) % W;  // its physical slot
+      const int len = sk + W - first;                       // masked ring slots
+      auto take = [&](int x, int y) {                       // physical slots [x, y)
+        const int t0 = (x + 31) / 32, t1 = y / 32;
+        if (t1 - t0 > s.skip_n) {
+          s.skip_t0 = t0;
+          s.skip_n = t1 - t0;
+        }
+      };
+      if (a + len <= sk + W) {
+        take(a, a + len);
+      } else {
+        take(a, sk + W);
+        take(sk, sk + (a + len - (sk + W)));
+      }
+      // the last tile may be partial: only whole tiles below n_scan are skipped
+      if (s.skip_t0 + s.skip_n > s.n_scan / 32) s.skip_n = s.n_scan / 32 - s.skip_t0;
+      if (s.skip_n < 0) s.skip_n = 0;
+      s.n_tiles -= s.skip_n;
+    }
+  }
   const int cus = num_cus > 0 ? num_cus : 256;
   s.waves = (L.D == 128 && s.nset == 1 && (long)s.n_tiles * L.kv_heads >= 8L * cus) ? 8 : 4;
   int tps = (s.n_tiles * L.kv_heads + cus - 1) / cus;
@@ -1438,6 +1472,8 @@ static hipError_t launch_cfg(const LayerView& L, const AttnArgs& a, hipStream_t 
   p.n_scan = sp.n_scan;
   p.phys_limit = sp.phys_limit;
   p.n_tiles = sp.n_tiles;
+  p.skip_t0 = sp.skip_t0;
+  p.skip_n = sp.skip_n;
   p.tiles_per_split = sp.tiles_per_split;
   p.n_splits = sp.n_splits;
   const int units = R * (D / 64);
