@@ -97,6 +97,44 @@ def test_c4_sinks_q8(dev):
     c.close()
 
 
+@pytest.mark.parametrize("steps,batch,verify", [(40, 7, 1), (90, 13, 5), (23, 31, 3), (7, 97, 2), (2, 500, 1),
+                                                 (3, 700, 3)])
+def test_sinks_masked_room_not_scanned(dev, steps, batch, verify):
+    """Sink mode after the ring wrapped, at several ring origins and amounts of room: the ring
+    slots past the last row's position are masked for every row, and the decode kernel does not
+    scan their longest run of whole tiles (in one piece, or wrapping across the ring's end: the
+    large batches leave room on both sides of it, the longer run before it (2, 500) or after it
+    (3, 700)); the output matches the oracle over the logical slots."""
+    KV, H, D, sinks, window = 8, 32, 128, 4, 1024
+    max_seq = sinks + window
+    c = E.KvCache(1, KV, D, "f16", max_seq_len=max_seq, overflow="sinks", sink_tokens=sinks)
+    fill = 900
+    for _ in range(steps):
+        fill = c.evict_for(fill, batch) + batch
+    fill = c.evict_for(fill, verify)
+    head, evicted = c.ring_state()
+    assert head != 0 and evicted > 0
+    rng = np.random.default_rng(steps * 1000 + batch)
+    k = rng.standard_normal((fill + verify, KV, D)).astype(np.float32)
+    v = rng.standard_normal((fill + verify, KV, D)).astype(np.float32)
+    q = rng.standard_normal((verify, H, D)).astype(np.float32)
+    cos_d, sin_d, cos, sin = rope_dev(1e4, D, max_seq)
+    c.set_rope(cos_d, sin_d)
+    ones = t(np.ones(D, np.float32))
+    E.qkv_prologue(c, 0, None, t(k[:fill]), t(v[:fill]), fill, H, None, ones, 1e-6, cos_d, sin_d, D, 0, 0)
+    qr = E.qkv_prologue(c, 0, t(q), t(k[fill:]), t(v[fill:]), verify, H, ones, ones, 1e-6, cos_d, sin_d, D,
+                        fill, fill)
+    out = E.attention(c, 0, qr, verify, H, fill)
+    torch.cuda.synchronize()
+    kq, vq, _, _ = export_k_v(c, 0, 0, fill + verify)
+    kk = ref.rope_apply(kq.astype(np.float32), cos, sin, np.arange(fill + verify))
+    exp = ref.attention(qr.cpu().numpy(), kk, vq.astype(np.float32), fill)
+    room = max_seq - (fill + verify)
+    assert room >= 64  # at least one whole tile of room
+    assert rel_err(out.cpu().numpy(), exp) <= 2e-3 and cosine(out.cpu().numpy(), exp) > 0.99999
+    c.close()
+
+
 @pytest.mark.parametrize("S", [1, 4, 40])
 def test_sinks_before_eviction_equal_plain_cache_f32(dev, S):
     """Before the first eviction the sink-mode cache (unroped keys, rotated at read) gives
