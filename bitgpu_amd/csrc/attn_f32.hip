@@ -115,7 +115,7 @@ __global__ __launch_bounds__(256) void attn_f32_split_kernel(LayerView L, AttnAr
       for (int i = 0; i < DQ; i++) {
         const float other = xor32(k[i]);
         const float rv = g < 2 ? -other : other;
-        k[i] = __fadd_rn(__fmul_rn(k[i], ct[i]), __fmul_rn(rv, st[i]));
+        k[i] = add_rn(mul_rn(k[i], ct[i]), mul_rn(rv, st[i]));
       }
     }
     float x[RM];

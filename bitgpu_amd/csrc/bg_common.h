@@ -63,13 +63,26 @@ struct Ring {
   }
 };
 
+// One IEEE-rounded product / sum that is never fused into an fma with its neighbour. The library
+// is compiled with contraction on (hipcc's default), and __fmul_rn / __fadd_rn are plain
+// operators in this toolchain, so a * b + c through them still becomes one fma; contraction is
+// off inside these two.
+__device__ inline float mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a * b;
+}
+__device__ inline float add_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a + b;
+}
+
 // ---- q8 pack: WGSL pack4x8snorm on a block-scaled value (shaders/copy_kv8.wgsl:24-40) ----
-// code = floor(0.5 + 127 * clamp(v / s, -1, 1)); explicit _rn intrinsics keep every step one
-// IEEE rounding (no contraction into an FMA, correctly rounded division).
+// code = floor(0.5 + 127 * clamp(v / s, -1, 1)), every step one IEEE rounding (a correctly
+// rounded division; the product and the sum not fused).
 __device__ inline int q8_code(float v, float s) {
   float e = __fdiv_rn(v, s);
   e = fminf(fmaxf(e, -1.0f), 1.0f);
-  float t = __fadd_rn(__fmul_rn(127.0f, e), 0.5f);
+  float t = add_rn(mul_rn(127.0f, e), 0.5f);
   return (int)floorf(t);
 }
 __device__ inline float q8_scale_of(float absmax) { return fmaxf(absmax, 1e-30f); }

@@ -4,8 +4,10 @@
 //
 // Arithmetic follows the reference kernels: y = x * inverseSqrt(sum(x^2) / D + eps) * gamma as
 // two rounded products (shaders/rmsnorm_rope_sg.wgsl:24,28) and y*cos + rot*sin as two rounded
-// products and a rounded sum (tools/reference.py:149-152; shaders/rmsnorm_rope_sg.wgsl:32), no
-// FMA contraction.
+// products and a rounded sum (tools/reference.py:149-152; shaders/rmsnorm_rope_sg.wgsl:32), none
+// of them fused into an fma (mul_rn / add_rn).
+// The rotate_half partner of a lane's dims is lane l ^ (rot / 8) of the row (a lane exchange)
+// when that is 8, 16 or 32 lanes, else it is read back from the row staged in LDS.
 #pragma once
 
 #include "bg_kernels.h"
@@ -17,15 +19,60 @@ template <int D, int LPR>
 __device__ inline float row_inv_rms(const float (&x)[4], float eps) {
   float ss = 0.0f;
 #pragma unroll
-  for (int e = 0; e < 4; e++) ss = __fadd_rn(ss, __fmul_rn(x[e], x[e]));
+  for (int e = 0; e < 4; e++) ss = add_rn(ss, mul_rn(x[e], x[e]));
   ss = group_sum<LPR>(ss);
   // ss / D is exact as a product: D is a power of two
-  return rsqrtf(__fadd_rn(ss * (1.0f / D), eps));
+  return rsqrtf(add_rn(ss * (1.0f / D), eps));
 }
 
 __device__ inline void row_scale(float (&x)[4], float inv, const float (&g)[4]) {
 #pragma unroll
-  for (int e = 0; e < 4; e++) x[e] = __fmul_rn(__fmul_rn(x[e], inv), g[e]);
+  for (int e = 0; e < 4; e++) x[e] = mul_rn(mul_rn(x[e], inv), g[e]);
+}
+
+// The rotate_half partners of this lane's dims (x[d + half] below half, x[d - half] above) by a
+// lane exchange: lane l ^ half/4 holds them when half is a multiple of 4 and half/4 is
+// 8 (DPP row_ror:8 inside a 16-lane row), 16 (v_permlane16_swap) or 32 lanes (v_permlane32_swap);
+// false for other widths. Every lane of the wave must take part (rot is wave-uniform); rows are
+// aligned to their D/4 lanes, so the partner lies in the same row.
+constexpr int kDppRor8 = 0x128;
+__device__ inline bool rope_partner_lanes(const float (&x)[4], int rot, float (&p)[4]) {
+  const int half = rot >> 1;
+  if ((half & 3) != 0) return false;
+  const int h4 = half >> 2;
+  if (h4 == 16) {
+    const bool odd = (__lane_id() & 16) != 0;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const float2 r = pair16(x[e]);
+      p[e] = odd ? r.x : r.y;
+    }
+    return true;
+  }
+  if (h4 == 32) {
+#pragma unroll
+    for (int e = 0; e < 4; e++) p[e] = xor32(x[e]);
+    return true;
+  }
+  if (h4 == 8) {
+#pragma unroll
+    for (int e = 0; e < 4; e++) p[e] = dpp_mov<kDppRor8>(x[e]);
+    return true;
+  }
+  return false;
+}
+
+// Rotate this lane's dims 4c..4c+3 (< rot) with the partners p from rope_partner_lanes: the
+// rotate_half value is -p (d < half) or p
+__device__ inline void row_rope_lanes(float (&x)[4], const float (&p)[4], int c, int rot, const float (&cs)[4],
+                                      const float (&sn)[4]) {
+  const int half = rot >> 1;
+  if (4 * c >= rot) return;
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    const float rv = 4 * c < half ? -p[e] : p[e];
+    x[e] = add_rn(mul_rn(x[e], cs[e]), mul_rn(rv, sn[e]));
+  }
 }
 
 // Rotate this lane's dims 4c..4c+3 (< rot); `row` is the normed row in LDS, which supplies the
@@ -39,7 +86,7 @@ __device__ inline void row_rope(float (&x)[4], const float* row, int c, int rot,
     const int d = 4 * c + e;
     if (d < rot) {
       const float rv = d < half ? -row[d + half] : row[d - half];
-      x[e] = __fadd_rn(__fmul_rn(x[e], cs[e]), __fmul_rn(rv, sn[e]));
+      x[e] = add_rn(mul_rn(x[e], cs[e]), mul_rn(rv, sn[e]));
     }
   }
 }

@@ -33,7 +33,8 @@
 //           NaN and raises the cache's host-visible error word (bg_attention then returns
 //           BG_E_DEVICE and resets the workspace).
 // Sink mode reads unroped K and rotates it at read by the slot's logical (or absolute) position
-// (attention_sg_roll.wgsl:40-51), in f32 before the f16 conversion.
+// (attention_sg_roll.wgsl:40-51), in f32 (x*c - y*s with the c product fused into the sum) before
+// the f16 conversion.
 #include <algorithm>
 #include <map>
 #include <mutex>
@@ -578,7 +579,9 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
             }
             // the products with s as fma(x, s, +0) (the same value as x * s but for the sign of
             // a zero, which the sum below cannot see): the f16 x then enters a mixed-precision
-            // fma directly instead of being converted first
+            // fma directly instead of being converted first. The product with c and the sum are
+            // contracted into that fma (one f32 rounding where the reference's rope has two;
+            // the result is rounded to f16 at once, so the keys match to the f16 rounding)
             const float bs = __builtin_fmaf(b2[e], s, 0.0f), as = __builtin_fmaf(a[e], s, 0.0f);
             r0.h[e] = (_Float16)__fadd_rn(__fmul_rn(a[e], c), -bs);
             r1.h[e] = (_Float16)__fadd_rn(__fmul_rn(b2[e], c), as);

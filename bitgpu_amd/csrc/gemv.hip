@@ -18,15 +18,18 @@
 //           (eight 16-byte loads from LDS or memory, reused by the wave's rows) and the word's
 //           signs flip their sign bits (one xor each), four partial sums per word. Either way
 //           times the word's block scale; a DPP / permlane wave sum finishes the row. With the
-//           table (at most two tiles) both tiles' weights are issued before it is built; longer
+//           table (at most two tiles) x is loaded first and both tiles' weights are issued
+//           before the table is built, so it is built under their latency; longer
 //           rows keep two tiles' loads (the rows' words and scales, x) in flight, the next tile
 //           issued before the current one's arithmetic. The residual is loaded at the start.
 //   fused   the qkv kernel's workgroups own 32 rows of one head; all but the head's last one
 //           store their raw rows into the cache's gather buffer (the XCD's L2 when the head's
 //           workgroups share an XCD) and are done; the last one polls them in (no arrival
-//           ticket, no store acknowledgement: 6.66 -> 5.9 us at the 8B shape), normalizes and
-//           ropes the head (Q -> q_out; K -> the cache row, unroped in sink mode) or stores it
-//           (V), with the fused prologue's row arithmetic (bg_qkrow.h).
+//           ticket, no store acknowledgement: 6.66 -> 5.9 us at the 8B shape), writes the
+//           empty markers back at once, normalizes and ropes the head (Q -> q_out; K -> the
+//           cache row, unroped in sink mode) or stores it (V), with the fused prologue's row
+//           arithmetic (bg_qkrow.h; the rope partner by a lane exchange). Markers first, the
+//           lane exchange and x before the weights: 5.65 -> 5.30 us.
 #include <map>
 #include <mutex>
 
@@ -66,33 +69,36 @@ __host__ __device__ constexpr size_t gemv_lut_bytes(int K) { return (size_t)K * 
 // The nibble table: lut[(16 g + e) W + w] = sum over k < 4 of (bit k of e set ? +x : -x) of
 // x[32 w + 4 g + k], summed as (k0, k1) + (k2, k3): every signed combination of a nibble's four
 // x values (bit set = weight +1, as in the word loop). W-fastest, so the lanes' reads (one word
-// each) fall on distinct banks. The kGemvThreads threads of the workgroup build it (at most 2 (word,
-// nibble) pairs each at K <= kLutMaxK) in two parts: in the GEMV the x loads are issued before
-// the weight loads (vector-memory waits retire in issue order, so the build then waits for x alone
-// and runs under the weights' latency), the table is written after them, then a barrier.
-constexpr int kLutPairsPerThread = 8 * (kLutMaxK / 32) / kGemvThreads;
+// each) fall on distinct banks. The NT threads of the workgroup build it (8 K / 32 / NT (word,
+// nibble) pairs each at most) in two parts: the x loads are issued before the weight loads
+// (vector-memory waits retire in issue order, so the build then waits for x alone and runs under
+// the weights' latency), the table is written after them, then a barrier.
+template <int NT>
 struct LutX {
-  float4 v[kLutPairsPerThread];
+  static constexpr int kPairs = 8 * (kLutMaxK / 32) / NT;
+  float4 v[kPairs];
 };
 // pair i = g W + w (i < 8 W <= 1024): g = floor(i * ceil(2^20 / W) / 2^20), exact for W < 1000
 __device__ __forceinline__ int lut_pair_g(int i, unsigned inv_w) { return (int)(__umul24((unsigned)i, inv_w) >> 20); }
-__device__ __forceinline__ void gemv_lut_load(const float* __restrict__ x, int K, LutX& X) {
+template <int NT>
+__device__ __forceinline__ void gemv_lut_load(const float* __restrict__ x, int K, LutX<NT>& X) {
   const int W = K >> 5;
   const unsigned inv_w = ((1u << 20) + W - 1) / W;
 #pragma unroll
-  for (int j = 0; j < kLutPairsPerThread; j++) {
-    const int i = threadIdx.x + kGemvThreads * j;
+  for (int j = 0; j < LutX<NT>::kPairs; j++) {
+    const int i = threadIdx.x + NT * j;
     const int ic = i < 8 * W ? i : 8 * W - 1;  // unconditional load, as for the weights
     const int g = lut_pair_g(ic, inv_w), w = ic - g * W;
     X.v[j] = *(const float4*)(x + 32 * w + 4 * g);
   }
 }
-__device__ __forceinline__ void gemv_lut_write(const LutX& X, float* lut, int K) {
+template <int NT>
+__device__ __forceinline__ void gemv_lut_write(const LutX<NT>& X, float* lut, int K) {
   const int W = K >> 5;
   const unsigned inv_w = ((1u << 20) + W - 1) / W;
 #pragma unroll
-  for (int j = 0; j < kLutPairsPerThread; j++) {
-    const int i = threadIdx.x + kGemvThreads * j;
+  for (int j = 0; j < LutX<NT>::kPairs; j++) {
+    const int i = threadIdx.x + NT * j;
     if (i < 8 * W) {
       const int g = lut_pair_g(i, inv_w), w = i - g * W;
       const float4 v = X.v[j];
@@ -105,27 +111,9 @@ __device__ __forceinline__ void gemv_lut_write(const LutX& X, float* lut, int K)
   }
   __syncthreads();
 }
-// the fused qkv kernel builds its table in one loop after both tiles' weight loads (measured
-// faster there than the two-part order; 5.84 -> 5.68 us with the second tile issued before the
-// build rather than after it)
-__device__ __forceinline__ void gemv_build_lut(const float* __restrict__ x, float* lut, int K) {
-  const int W = K >> 5;
-  for (int i = threadIdx.x; i < 8 * W; i += blockDim.x) {
-    const int w = i % W, g = i / W;
-    const float4 v = *(const float4*)(x + 32 * w + 4 * g);
-    const float a[4] = {-v.x - v.y, v.x - v.y, v.y - v.x, v.x + v.y};
-    const float b[4] = {-v.z - v.w, v.z - v.w, v.w - v.z, v.z + v.w};
-    float* d = lut + (size_t)(16 * g) * W + w;
-#pragma unroll
-    for (int e = 0; e < 16; e++) d[(size_t)e * W] = a[e & 3] + b[e >> 2];
-  }
-  __syncthreads();
-}
-
 // BF: every load unconditional (clamped address, the value zeroed after), so no branch: the wait
 // counts stay exact and a later wait for loads issued before these does not drain them (the
-// GEMV's table build then waits for its x loads alone); otherwise rows past the end are not
-// loaded (measured faster for the fused qkv kernel, which builds its table after these loads)
+// table build then waits for its x loads alone); otherwise rows past the end are not loaded
 template <int RW, bool BF = false>
 __device__ __forceinline__ void gemv_load_w(GemvTile<RW>& T, int W, int NB, const uint32_t* __restrict__ sign,
                                             const float* __restrict__ scales, int n0, int n_rows, int t, int lane) {
@@ -266,8 +254,8 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
   const int n0 = (blockIdx.x * kGemvWaves + wave) * kGemvRW;
   // lane r < kGemvRW stores row n0 + r: its residual and the first tile's weights are loaded
   // before x is staged
-  LutX X;
-  if constexpr (XM == kXLut) gemv_lut_load(a.x, a.K, X);
+  LutX<kGemvThreads> X;
+  if constexpr (XM == kXLut) gemv_lut_load<kGemvThreads>(a.x, a.K, X);
   const float res = (a.resid && lane < kGemvRW && n0 + lane < N) ? a.resid[n0 + lane] : 0.0f;
   GemvTile<kGemvRW> A;
   gemv_load_w<kGemvRW, XM == kXLut>(A, a.K >> 5, a.K >> 7, a.sign, a.scales, n0, N, 0, lane);
@@ -278,7 +266,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
     const int W = a.K >> 5;
     GemvTile<kGemvRW> B;
     gemv_load_w<kGemvRW, true>(B, W, a.K >> 7, a.sign, a.scales, n0, N, 1, lane);
-    gemv_lut_write(X, xs, a.K);
+    gemv_lut_write<kGemvThreads>(X, xs, a.K);
     if (n0 >= N) return;  // wave-uniform
     gemv_lut_rows<kGemvRW>(A, B, xs, W, lane, tot);
   } else {
@@ -334,6 +322,9 @@ hipError_t launch_gemv(const GemvArgs& a, hipStream_t st) {
 // 32 rows of one head a workgroup (16 waves of kGemvRW rows): the 8B shape's 192 workgroups one
 // a CU, 6.7 us against 384 of 16 rows, two on half the CUs (7.3 us), or 96 of 64 rows (7.5 us)
 constexpr int kQkvRowsPerWg = 32;
+// s_waitcnt vmcnt(0) with expcnt and lgkmcnt left alone (gfx9 encoding: vmcnt bits 3:0 and 15:14,
+// expcnt 6:4, lgkmcnt 11:8)
+constexpr int kWaitVm0 = 0x0F70;
 constexpr int kQkvThreads = 64 * kQkvRowsPerWg / kGemvRW;
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
@@ -343,9 +334,9 @@ size_t qkv_proj_raw_floats(int heads, int D) { return (size_t)heads * D; }
 // Each head's D rows are G = D / 32 parts, one workgroup each. Parts 0 .. G-2 store their raw rows
 // into the gather buffer and are done; the finishing part G-1 keeps its own rows in LDS, polls the
 // others' until none holds the empty marker (the data is the completion signal: no ticket, no
-// store acknowledgement to wait for), normalizes, ropes and stores the row with the prologue's
-// arithmetic (bg_qkrow.h: bit-identical to bg_gemv_split followed by bg_qkv_prologue), and writes
-// the marker back (written through: the next launch's parts may run on another XCD). The finisher
+// store acknowledgement to wait for), writes the marker back (written through: the next launch's
+// parts may run on another XCD), then normalizes, ropes and stores the row with the prologue's
+// arithmetic (bg_qkrow.h: bit-identical to bg_gemv_split followed by bg_qkv_prologue). The finisher
 // is its head's highest workgroup index, so the parts it waits on are dispatched before it and
 // finish on their own; the wait is still bounded (a finisher that gives up stores NaN and raises
 // the cache's error word). The parts of a head share blockIdx mod 8 when the head count allows it,
@@ -380,14 +371,18 @@ __global__ __launch_bounds__(kQkvThreads) void qkv_proj_kernel(LayerView L, QkvP
   {
     const int n0 = wg_n0 + wave * kGemvRW;
     GemvTile<kGemvRW> A;
-    gemv_load_w<kGemvRW>(A, a.K >> 5, a.K >> 7, a.sign, a.scales, n0, N, 0, lane);
     float tot[kGemvRW];
     if constexpr (XM == kXLut) {
+      // x first, then both tiles' weights (branch-free), so the table is built under their latency
+      LutX<kQkvThreads> X;
+      gemv_lut_load<kQkvThreads>(a.x, a.K, X);
       GemvTile<kGemvRW> B;
-      gemv_load_w<kGemvRW>(B, a.K >> 5, a.K >> 7, a.sign, a.scales, n0, N, 1, lane);
-      gemv_build_lut(a.x, xs, a.K);
+      gemv_load_w<kGemvRW, true>(A, a.K >> 5, a.K >> 7, a.sign, a.scales, n0, N, 0, lane);
+      gemv_load_w<kGemvRW, true>(B, a.K >> 5, a.K >> 7, a.sign, a.scales, n0, N, 1, lane);
+      gemv_lut_write<kQkvThreads>(X, xs, a.K);
       gemv_lut_rows<kGemvRW>(A, B, xs, a.K >> 5, lane, tot);
     } else {
+      gemv_load_w<kGemvRW>(A, a.K >> 5, a.K >> 7, a.sign, a.scales, n0, N, 0, lane);
       if constexpr (XM == kXLds) gemv_stage_x(a.x, xs, a.K);
       gemv_rows<kGemvRW, XM, false>(A, a.x, xs, a.K, a.sign, a.scales, n0, N, lane, tot);
     }
@@ -444,6 +439,16 @@ __global__ __launch_bounds__(kQkvThreads) void qkv_proj_kernel(LayerView L, QkvP
     gave_up = missing;
   }
   gave_up = __any(gave_up);
+  // the empty marker back into the slots read, as soon as they are in registers (before the
+  // row's stores: a marker store issued after them would wait for their acknowledgement, since
+  // it reuses their data registers). Every load has arrived here (the poll waited for its own,
+  // issued after gamma and the tables); the explicit vmcnt(0) says so to the compiler, which
+  // would otherwise wait for the marker store's acknowledgement before using gamma.
+  __builtin_amdgcn_s_waitcnt(kWaitVm0);
+  if (writer && !mine) {
+    const u32x4_t empty4 = {kWorkspaceEmpty, kWorkspaceEmpty, kWorkspaceEmpty, kWorkspaceEmpty};
+    __builtin_amdgcn_raw_buffer_store_b128(empty4, rs, 16 * c, 0, kSC1);
+  }
   if (gave_up) {
 #pragma unroll
     for (int e = 0; e < 4; e++) x[e] = __builtin_nanf("");
@@ -451,11 +456,17 @@ __global__ __launch_bounds__(kQkvThreads) void qkv_proj_kernel(LayerView L, QkvP
   if (isq || isk) {
     row_scale(x, row_inv_rms<D, LPR>(x, a.eps), g);
     if (rope) {
-      if (writer) *(float4*)(rrow + 4 * c) = make_float4(x[0], x[1], x[2], x[3]);
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      row_rope(x, rrow, c, a.rot_dim, cs, sn);
+      // the rotate_half partners by a lane exchange where the width allows it, else through LDS
+      float pr[4];
+      if (rope_partner_lanes(x, a.rot_dim, pr)) {
+        row_rope_lanes(x, pr, c, a.rot_dim, cs, sn);
+      } else {
+        if (writer) *(float4*)(rrow + 4 * c) = make_float4(x[0], x[1], x[2], x[3]);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        row_rope(x, rrow, c, a.rot_dim, cs, sn);
+      }
     }
     if (isq) {
       if (writer) *(float4*)(a.q_out + head * D + 4 * c) = make_float4(x[0], x[1], x[2], x[3]);
@@ -465,11 +476,6 @@ __global__ __launch_bounds__(kQkvThreads) void qkv_proj_kernel(LayerView L, QkvP
     }
   } else {
     if (D == 256 || writer) store_v4<D, DT>(L, L.ring.phys(a.slot), head - a.H - KV, x, c);
-  }
-  // the empty marker back into the slots read, last
-  if (writer && !mine) {
-    const u32x4_t empty4 = {kWorkspaceEmpty, kWorkspaceEmpty, kWorkspaceEmpty, kWorkspaceEmpty};
-    __builtin_amdgcn_raw_buffer_store_b128(empty4, rs, 16 * c, 0, kSC1);
   }
   if (gave_up && lane == 0) __hip_atomic_store(a.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }

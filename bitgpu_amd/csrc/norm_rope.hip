@@ -7,9 +7,10 @@
 //   Q / K rows 8 (D=128) or 4 (D=256) rows per wave: a lane owns 4 consecutive dims (one
 //              16-byte load), a row spans D/4 lanes; every load (rows and the lanes' cos/sin
 //              entries) is issued before any compute; the sum of squares is a reduction over
-//              the row's lanes (DPP / permlane), and the rotate_half partner (d +- rot/2) is read
-//              back through the wave's own LDS rows (any even rot_dim, full or partial, one code
-//              path; no workgroup barrier). Q leaves as one 16-byte store a lane, K as 16 / 8 /
+//              the row's lanes (DPP / permlane), and the rotate_half partner (d +- rot/2) comes
+//              from lane l ^ rot/8 by a lane exchange when that is 8, 16 or 32 lanes (rot_dim
+//              64, 128, 256), else it is read back through the wave's own LDS rows (any even
+//              rot_dim, full or partial; no workgroup barrier). Q leaves as one 16-byte store a lane, K as 16 / 8 /
 //              4 bytes (f32 / f16 / q8 codes, plus one scale per 32 dims).
 //   V row      one position, stored into the transposed V tile (single rows: a partial group at
 //              either end of the range, every row in sink mode).
@@ -214,7 +215,7 @@ __global__ __launch_bounds__(256) void qkv_prologue_kernel(LayerView L, Prologue
       }
     }
     // RMSNorm as the reference kernel: y = x * inverseSqrt(sum(x^2) / D + eps) * gamma
-    // (shaders/rmsnorm_rope_sg.wgsl:24,28), no FMA contraction
+    // (shaders/rmsnorm_rope_sg.wgsl:24,28), no FMA contraction (bg_qkrow.h)
     float gq[4], gk[4];
     {
       const float4 g4 = a.q_gamma ? *(const float4*)(a.q_gamma + 4 * c) : make_float4(0, 0, 0, 0);
@@ -228,18 +229,31 @@ __global__ __launch_bounds__(256) void qkv_prologue_kernel(LayerView L, Prologue
       const int r = item * RB + RPI * i + h;
       const bool isq = r < gr.nq;
       row_scale(x[i], row_inv_rms<D, LPR>(x[i], a.eps), isq ? gq : gk);
-      *(float4*)(rb + (RPI * i + h) * D + 4 * c) = make_float4(x[i][0], x[i][1], x[i][2], x[i][3]);
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // the rotate_half partners by a lane exchange (every lane, before the per-row branches) where
+    // the rotary width allows it, else through the wave's LDS rows
+    float pr[NI][4];
+    bool lanes = true;
+#pragma unroll
+    for (int i = 0; i < NI; i++) lanes = rope_partner_lanes(x[i], rot, pr[i]);
+    if (!lanes) {
+#pragma unroll
+      for (int i = 0; i < NI; i++)
+        *(float4*)(rb + (RPI * i + h) * D + 4 * c) = make_float4(x[i][0], x[i][1], x[i][2], x[i][3]);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
 #pragma unroll
     for (int i = 0; i < NI; i++) {
       const int r = item * RB + RPI * i + h;
       const bool isq = r < gr.nq;
       // y*cos + rot*sin as two rounded products and a rounded sum (tools/reference.py:149-152;
       // shaders/rmsnorm_rope_sg.wgsl:32); rot = -x[d + half] below half, x[d - half] above
-      if (isq || gr.rope_k) row_rope(x[i], rb + (RPI * i + h) * D, c, rot, cs[i < NT ? i : 0], sn[i < NT ? i : 0]);
+      if (isq || gr.rope_k) {
+        if (lanes) row_rope_lanes(x[i], pr[i], c, rot, cs[i < NT ? i : 0], sn[i < NT ? i : 0]);
+        else row_rope(x[i], rb + (RPI * i + h) * D, c, rot, cs[i < NT ? i : 0], sn[i < NT ? i : 0]);
+      }
       if (r < nqk) {
         if (isq) {
           st_stream16f(a.q_out + (size_t)r * D + 4 * c, x[i][0], x[i][1], x[i][2], x[i][3]);

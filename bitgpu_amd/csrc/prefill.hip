@@ -264,8 +264,8 @@ struct Stager {
 #pragma unroll
         for (int e = 0; e < 4; e++) {
           const float x = a[4 * i + e], y = b[4 * i + e];
-          a[4 * i + e] = __fadd_rn(__fmul_rn(x, c4[e]), __fmul_rn(-y, s4[e]));
-          b[4 * i + e] = __fadd_rn(__fmul_rn(y, c4[e]), __fmul_rn(x, s4[e]));
+          a[4 * i + e] = add_rn(mul_rn(x, c4[e]), mul_rn(-y, s4[e]));
+          b[4 * i + e] = add_rn(mul_rn(y, c4[e]), mul_rn(x, s4[e]));
         }
       }
     }

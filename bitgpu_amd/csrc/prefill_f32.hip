@@ -147,8 +147,9 @@ __global__ __launch_bounds__(256) void prefill_f32_kernel(F32PrefillParams p) {
         ri = ri < L.rope_positions ? ri : 0;
         const float4 cs = *(const float4*)(L.cos_tab + (size_t)ri * (D / 2) + c);
         const float4 sn = *(const float4*)(L.sin_tab + (size_t)ri * (D / 2) + c);
-        auto rot = [](float a, float b, float co, float si) { return __fadd_rn(__fmul_rn(a, co), __fmul_rn(-b, si)); };
-        auto rot2 = [](float b, float a, float co, float si) { return __fadd_rn(__fmul_rn(b, co), __fmul_rn(a, si)); };
+        // two rounded products and a rounded sum, not fused
+        auto rot = [](float a, float b, float co, float si) { return add_rn(mul_rn(a, co), mul_rn(-b, si)); };
+        auto rot2 = [](float b, float a, float co, float si) { return add_rn(mul_rn(b, co), mul_rn(a, si)); };
         lo = make_float4(rot(kr[i][0].x, kr[i][1].x, cs.x, sn.x), rot(kr[i][0].y, kr[i][1].y, cs.y, sn.y),
                          rot(kr[i][0].z, kr[i][1].z, cs.z, sn.z), rot(kr[i][0].w, kr[i][1].w, cs.w, sn.w));
         hi = make_float4(rot2(kr[i][1].x, kr[i][0].x, cs.x, sn.x), rot2(kr[i][1].y, kr[i][0].y, cs.y, sn.y),
