@@ -966,6 +966,7 @@ int32_t bg_qkv_proj_prologue(bg_kv_cache* c, int32_t layer, const float* x, int3
   a.spin_limit = g_merge_spin.load(std::memory_order_relaxed);
   const int xs = xcd_state(c->device);
   a.n_xcd = xs > 0 ? xs : 0;
+  a.num_cus = c->num_cus;
   hipError_t e = bg::launch_qkv_proj(view(c, layer), a, (hipStream_t)stream);
   return e == hipSuccess ? BG_OK : hip_fail(e, "qkv projection launch");
 }

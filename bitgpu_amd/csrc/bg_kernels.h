@@ -76,6 +76,7 @@ struct QkvProjArgs {
   unsigned* err;                   // host-visible error word: a finisher's bounded wait gave up
   int spin_limit;                  // poll rounds before a finisher gives up (0: 2^20)
   int n_xcd;                       // > 0: workgroups go to XCDs round robin (see AttnArgs)
+  int num_cus;                     // compute units: 24-row workgroups when 32-row ones leave some idle
 };
 // raw-row floats the fused projection's gather buffer holds (heads of every kind x head_dim)
 size_t qkv_proj_raw_floats(int heads, int D);

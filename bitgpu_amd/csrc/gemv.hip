@@ -29,7 +29,8 @@
 //           empty markers back at once, normalizes and ropes the head (Q -> q_out; K -> the
 //           cache row, unroped in sink mode) or stores it (V), with the fused prologue's row
 //           arithmetic (bg_qkrow.h; the rope partner by a lane exchange). Markers first, the
-//           lane exchange and x before the weights: 5.65 -> 5.30 us.
+//           lane exchange and x before the weights: 5.65 -> 5.30 us; 24-row workgroups over
+//           every CU (a workgroup may hold the end of one head and the start of the next): 5.19.
 #include <map>
 #include <mutex>
 
@@ -69,13 +70,13 @@ __host__ __device__ constexpr size_t gemv_lut_bytes(int K) { return (size_t)K * 
 // The nibble table: lut[(16 g + e) W + w] = sum over k < 4 of (bit k of e set ? +x : -x) of
 // x[32 w + 4 g + k], summed as (k0, k1) + (k2, k3): every signed combination of a nibble's four
 // x values (bit set = weight +1, as in the word loop). W-fastest, so the lanes' reads (one word
-// each) fall on distinct banks. The NT threads of the workgroup build it (8 K / 32 / NT (word,
-// nibble) pairs each at most) in two parts: the x loads are issued before the weight loads
+// each) fall on distinct banks. The NT threads of the workgroup build it (ceil(8 K / 32 / NT)
+// (word, nibble) pairs each at most) in two parts: the x loads are issued before the weight loads
 // (vector-memory waits retire in issue order, so the build then waits for x alone and runs under
 // the weights' latency), the table is written after them, then a barrier.
 template <int NT>
 struct LutX {
-  static constexpr int kPairs = 8 * (kLutMaxK / 32) / NT;
+  static constexpr int kPairs = (8 * (kLutMaxK / 32) + NT - 1) / NT;
   float4 v[kPairs];
 };
 // pair i = g W + w (i < 8 W <= 1024): g = floor(i * ceil(2^20 / W) / 2^20), exact for W < 1000
@@ -319,67 +320,67 @@ hipError_t launch_gemv(const GemvArgs& a, hipStream_t st) {
 }
 
 // ---- fused decode qkv projection + prologue ---------------------------------------------------
-// 32 rows of one head a workgroup (16 waves of kGemvRW rows): the 8B shape's 192 workgroups one
-// a CU, 6.7 us against 384 of 16 rows, two on half the CUs (7.3 us), or 96 of 64 rows (7.5 us)
-constexpr int kQkvRowsPerWg = 32;
+// RPW rows a workgroup (RPW / kGemvRW waves): 32 (16 waves), or 24 (12 waves) when 32-row
+// workgroups would leave CUs idle (the 8B shape: 256 workgroups of 24 rows instead of 192 of 32,
+// 5.27 -> 5.19 us; the table reads are VALU-bound, so the rows a CU holds set that phase). 192 of
+// 32 rows measured 6.7 us against 384 of 16 rows, two on half the CUs (7.3 us), or 96 of 64 (7.5).
 // s_waitcnt vmcnt(0) with expcnt and lgkmcnt left alone (gfx9 encoding: vmcnt bits 3:0 and 15:14,
 // expcnt 6:4, lgkmcnt 11:8)
 constexpr int kWaitVm0 = 0x0F70;
-constexpr int kQkvThreads = 64 * kQkvRowsPerWg / kGemvRW;
+template <int RPW>
+constexpr int qkv_threads() { return 64 * RPW / kGemvRW; }
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 size_t qkv_proj_raw_floats(int heads, int D) { return (size_t)heads * D; }
 
-// Each head's D rows are G = D / 32 parts, one workgroup each. Parts 0 .. G-2 store their raw rows
-// into the gather buffer and are done; the finishing part G-1 keeps its own rows in LDS, polls the
-// others' until none holds the empty marker (the data is the completion signal: no ticket, no
-// store acknowledgement to wait for), writes the marker back (written through: the next launch's
-// parts may run on another XCD), then normalizes, ropes and stores the row with the prologue's
-// arithmetic (bg_qkrow.h: bit-identical to bg_gemv_split followed by bg_qkv_prologue). The finisher
-// is its head's highest workgroup index, so the parts it waits on are dispatched before it and
-// finish on their own; the wait is still bounded (a finisher that gives up stores NaN and raises
-// the cache's error word). The parts of a head share blockIdx mod 8 when the head count allows it,
-// so with round-robin placement they share an XCD and the raw rows stay in its L2.
-template <int D, int DT, int XM>
-__global__ __launch_bounds__(kQkvThreads) void qkv_proj_kernel(LayerView L, QkvProjArgs a) {
+// Workgroup v owns rows [v RPW, v RPW + RPW) of the [Q heads | K heads | V heads] x D output.
+// The workgroup holding a head's last row finishes that head: its rows of the head stay in LDS,
+// its rows of the next head (RPW < D: a workgroup can straddle two heads) and every other
+// workgroup's rows go into the gather buffer; the finisher polls the head's earlier rows until
+// none holds the empty marker (the data is the completion signal: no ticket, no store
+// acknowledgement to wait for), writes the marker back (written through: the next launch's
+// workgroups may run on another XCD), then normalizes, ropes and stores the row with the
+// prologue's arithmetic (bg_qkrow.h: bit-identical to bg_gemv_split followed by
+// bg_qkv_prologue). The rows a finisher waits on belong to lower workgroup indices, dispatched
+// before it, which finish on their own; the wait is still bounded (a finisher that gives up
+// stores NaN and raises the cache's error word). When the grid is a multiple of 8 and every
+// eighth of the rows is whole heads, blockIdx 8m + x is workgroup v = x (grid / 8) + m, so with
+// round-robin placement each XCD holds a run of whole heads and the raw rows stay in its L2.
+template <int D, int DT, int XM, int RPW>
+__global__ __launch_bounds__(qkv_threads<RPW>()) void qkv_proj_kernel(LayerView L, QkvProjArgs a) {
+  constexpr int NT = qkv_threads<RPW>();
   constexpr int LPR = D / 4;  // lanes per row in the epilogue
-  constexpr int G = D / kQkvRowsPerWg;
   constexpr int kSC1 = 16;    // cache policy sc1: agent scope
   extern __shared__ __align__(16) float xs[];
   __shared__ __align__(16) float rrow[D];
-  __shared__ __align__(16) float own[kQkvRowsPerWg];
+  __shared__ __align__(16) float own[RPW];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int KV = L.kv_heads;
   const int nq = a.H * D;
-  const int N = nq + 2 * KV * D;
-  // The G workgroups of a head share blockIdx.x % 8 when the grid is a multiple of 8 G: head
-  // (k / G) * 8 + x, part k % G for blockIdx.x = 8k + x (the 8B shape: 7.35 against 7.52 us with
-  // the arrival ticket this kernel used before)
-  int wgi = blockIdx.x;
-  const bool grouped = (gridDim.x & (8 * G - 1)) == 0;
-  if (grouped) {
-    const int x = blockIdx.x & 7, k = blockIdx.x >> 3;
-    wgi = ((k / G) * 8 + x) * G + k % G;
-  }
-  const int wg_n0 = wgi * kQkvRowsPerWg;
-  const int head = wg_n0 / D;  // 0 .. H-1: Q heads, then K heads, then V heads
-  const int part = wgi % G;
-  const bool finisher = part == G - 1;
-  // raw rows stay in the XCD's L2 when every part of the head shares it
+  const int N = nq + 2 * KV * D;  // gridDim.x * RPW
+  const int nwg = gridDim.x;
+  const bool grouped = (nwg & 7) == 0 && ((nwg >> 3) * RPW) % D == 0;
+  const int v = grouped ? (blockIdx.x & 7) * (nwg >> 3) + (blockIdx.x >> 3) : blockIdx.x;
+  const int r0 = v * RPW;
+  const int head = r0 / D;  // of the first row; 0 .. H-1: Q heads, then K heads, then V heads
+  const int hend = (head + 1) * D;
+  const bool finisher = r0 + RPW >= hend;  // holds the head's last row
+  const int own0 = r0 - head * D;          // the finisher's first dim of the head
+  // raw rows stay in the XCD's L2 when every workgroup of the head shares it
   const bool local = grouped && a.n_xcd == 8;
   {
-    const int n0 = wg_n0 + wave * kGemvRW;
+    const int n0 = r0 + wave * kGemvRW;
     GemvTile<kGemvRW> A;
     float tot[kGemvRW];
     if constexpr (XM == kXLut) {
       // x first, then both tiles' weights (branch-free), so the table is built under their latency
-      LutX<kQkvThreads> X;
-      gemv_lut_load<kQkvThreads>(a.x, a.K, X);
+      LutX<NT> X;
+      gemv_lut_load<NT>(a.x, a.K, X);
       GemvTile<kGemvRW> B;
       gemv_load_w<kGemvRW, true>(A, a.K >> 5, a.K >> 7, a.sign, a.scales, n0, N, 0, lane);
       gemv_load_w<kGemvRW, true>(B, a.K >> 5, a.K >> 7, a.sign, a.scales, n0, N, 1, lane);
-      gemv_lut_write<kQkvThreads>(X, xs, a.K);
+      gemv_lut_write<NT>(X, xs, a.K);
       gemv_lut_rows<kGemvRW>(A, B, xs, a.K >> 5, lane, tot);
     } else {
       gemv_load_w<kGemvRW>(A, a.K >> 5, a.K >> 7, a.sign, a.scales, n0, N, 0, lane);
@@ -388,13 +389,14 @@ __global__ __launch_bounds__(kQkvThreads) void qkv_proj_kernel(LayerView L, QkvP
     }
 #pragma unroll
     for (int r = 0; r < kGemvRW; r++) {
+      const int n = n0 + r;
       if (lane != r) continue;
-      if (finisher) {
-        own[wave * kGemvRW + r] = tot[r];
+      if (finisher && n < hend) {
+        own[n - r0] = tot[r];
       } else if (local) {
-        a.raw[n0 + r] = tot[r];  // into the XCD's L2
+        a.raw[n] = tot[r];  // into the XCD's L2
       } else {
-        st_coherent(a.raw + n0 + r, tot[r]);
+        st_coherent(a.raw + n, tot[r]);
       }
     }
   }
@@ -407,8 +409,7 @@ __global__ __launch_bounds__(kQkvThreads) void qkv_proj_kernel(LayerView L, QkvP
   const int c = lane % LPR;
   const bool writer = lane < LPR;
   const bool isq = head < a.H, isk = !isq && head < a.H + KV;
-  const int own0 = (G - 1) * kQkvRowsPerWg;  // the finisher's dims
-  const bool mine = 4 * c >= own0;
+  const bool mine = 4 * c >= own0;  // own0 is a multiple of 8
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(a.raw + (size_t)head * D, (short)0,
                                                                       D * 4, 0x00020000);
   // the row's gamma and rope tables are loaded before the wait, so the epilogue starts on arrival
@@ -480,36 +481,41 @@ __global__ __launch_bounds__(kQkvThreads) void qkv_proj_kernel(LayerView L, QkvP
   if (gave_up && lane == 0) __hip_atomic_store(a.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
-template <int D, int DT, int XM>
+template <int D, int DT, int XM, int RPW>
 static hipError_t launch_qkv_proj_k(const LayerView& L, const QkvProjArgs& a, dim3 g, size_t lds, hipStream_t st) {
   if constexpr (XM == kXLut) {
-    const hipError_t e = gemv_allow_lds((const void*)qkv_proj_kernel<D, DT, XM>, lds);
+    const hipError_t e = gemv_allow_lds((const void*)qkv_proj_kernel<D, DT, XM, RPW>, lds);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL((qkv_proj_kernel<D, DT, XM>), g, dim3(kQkvThreads), lds, st, L, a);
+  hipLaunchKernelGGL((qkv_proj_kernel<D, DT, XM, RPW>), g, dim3(qkv_threads<RPW>()), lds, st, L, a);
   return hipGetLastError();
 }
 
-template <int D, int XM>
+template <int D, int XM, int RPW>
 static hipError_t launch_qkv_proj_d(const LayerView& L, const QkvProjArgs& a, dim3 g, size_t lds, hipStream_t st) {
   switch (L.dtype) {
-    case KV_F32: return launch_qkv_proj_k<D, KV_F32, XM>(L, a, g, lds, st);
-    case KV_F16: return launch_qkv_proj_k<D, KV_F16, XM>(L, a, g, lds, st);
-    default: return launch_qkv_proj_k<D, KV_Q8, XM>(L, a, g, lds, st);
+    case KV_F32: return launch_qkv_proj_k<D, KV_F32, XM, RPW>(L, a, g, lds, st);
+    case KV_F16: return launch_qkv_proj_k<D, KV_F16, XM, RPW>(L, a, g, lds, st);
+    default: return launch_qkv_proj_k<D, KV_Q8, XM, RPW>(L, a, g, lds, st);
   }
 }
 
-template <int D>
+template <int D, int RPW>
 static hipError_t launch_qkv_proj_x(const LayerView& L, const QkvProjArgs& a, dim3 g, hipStream_t st) {
-  if (a.K <= kLutMaxK) return launch_qkv_proj_d<D, kXLut>(L, a, g, gemv_lut_bytes(a.K), st);
-  if (a.K <= kGemvLdsMaxK) return launch_qkv_proj_d<D, kXLds>(L, a, g, (size_t)(a.K / 32) * kXPad * sizeof(float), st);
-  return launch_qkv_proj_d<D, kXGlobal>(L, a, g, 0, st);
+  if (a.K <= kLutMaxK) return launch_qkv_proj_d<D, kXLut, RPW>(L, a, g, gemv_lut_bytes(a.K), st);
+  if (a.K <= kGemvLdsMaxK)
+    return launch_qkv_proj_d<D, kXLds, RPW>(L, a, g, (size_t)(a.K / 32) * kXPad * sizeof(float), st);
+  return launch_qkv_proj_d<D, kXGlobal, RPW>(L, a, g, 0, st);
 }
 
 hipError_t launch_qkv_proj(const LayerView& L, const QkvProjArgs& a, hipStream_t st) {
   const int N = (a.H + 2 * L.kv_heads) * L.D;
-  const dim3 g(N / kQkvRowsPerWg);
-  return L.D == 128 ? launch_qkv_proj_x<128>(L, a, g, st) : launch_qkv_proj_x<256>(L, a, g, st);
+  // 24-row workgroups (D = 128) when 32-row ones would leave CUs idle and the rows fall into 8
+  // runs of whole heads (one an XCD)
+  if (L.D == 128 && N / 32 < a.num_cus && N % (24 * 8) == 0 && (N / 8) % 128 == 0)
+    return launch_qkv_proj_x<128, 24>(L, a, dim3(N / 24), st);
+  const dim3 g(N / 32);
+  return L.D == 128 ? launch_qkv_proj_x<128, 32>(L, a, g, st) : launch_qkv_proj_x<256, 32>(L, a, g, st);
 }
 
 }  // namespace bg
