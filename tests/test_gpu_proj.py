@@ -76,10 +76,13 @@ def _qkv_case(dtype, H, KV, D, K, pos, seed, roll=False):
 
 
 @pytest.mark.parametrize("dtype", ["f16", "q8", "f32"])
-@pytest.mark.parametrize("H,KV,D", [(32, 8, 128), (16, 8, 128), (8, 2, 256)])
+@pytest.mark.parametrize("H,KV,D", [(32, 8, 128), (16, 8, 128), (8, 2, 256), (20, 2, 128), (24, 12, 128)])
 def test_qkv_proj_prologue_equals_unfused(dev, dtype, H, KV, D):
     """One launch (projection, Q norm+rope, K norm+rope into the cache, V append) equals the
-    projection followed by the prologue, bit for bit: q_out and every stored K / V byte."""
+    projection followed by the prologue, bit for bit: q_out and every stored K / V byte.
+    (32, 8), (20, 2) and (24, 12) at D=128 run 24-row workgroups (heads across workgroup
+    boundaries; 256 / 128 / 256 workgroups, the Q/K/V boundaries at different places), the
+    others 32-row ones."""
     K, pos = 4096, 777
     rng, sign, sc, x, gq, gk = _qkv_case(dtype, H, KV, D, K, pos, seed=H + KV + D)
     w = _dev_weight(sign, sc, K, H * D, KV * D, KV * D)
