@@ -30,7 +30,8 @@
 //           cache row, unroped in sink mode) or stores it (V), with the fused prologue's row
 //           arithmetic (bg_qkrow.h; the rope partner by a lane exchange). Markers first, the
 //           lane exchange and x before the weights: 5.65 -> 5.30 us; 24-row workgroups over
-//           every CU (a workgroup may hold the end of one head and the start of the next): 5.19.
+//           every CU (a workgroup may hold the end of one head and the start of the next): 5.19;
+//           the poll before the finisher's barrier: 4.85.
 #include <map>
 #include <mutex>
 
@@ -337,9 +338,10 @@ size_t qkv_proj_raw_floats(int heads, int D) { return (size_t)heads * D; }
 // Workgroup v owns rows [v RPW, v RPW + RPW) of the [Q heads | K heads | V heads] x D output.
 // The workgroup holding a head's last row finishes that head: its rows of the head stay in LDS,
 // its rows of the next head (RPW < D: a workgroup can straddle two heads) and every other
-// workgroup's rows go into the gather buffer; the finisher polls the head's earlier rows until
-// none holds the empty marker (the data is the completion signal: no ticket, no store
-// acknowledgement to wait for), writes the marker back (written through: the next launch's
+// workgroup's rows go into the gather buffer; the finisher's first wave polls the head's earlier
+// rows until none holds the empty marker (the data is the completion signal: no ticket, no store
+// acknowledgement to wait for) while its sibling waves finish their rows (it meets them at the
+// barrier only after the poll: 5.05 -> 4.85 us at the 8B shape), writes the marker back (written through: the next launch's
 // workgroups may run on another XCD), then normalizes, ropes and stores the row with the
 // prologue's arithmetic (bg_qkrow.h: bit-identical to bg_gemv_split followed by
 // bg_qkv_prologue). The rows a finisher waits on belong to lower workgroup indices, dispatched
@@ -355,7 +357,8 @@ __global__ __launch_bounds__(qkv_threads<RPW>()) void qkv_proj_kernel(LayerView 
   extern __shared__ __align__(16) float xs[];
   __shared__ __align__(16) float rrow[D];
   __shared__ __align__(16) float own[RPW];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // wave-uniform (scalar): the finisher's waves take different branches around one barrier
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int KV = L.kv_heads;
   const int nq = a.H * D;
   const int N = nq + 2 * KV * D;  // gridDim.x * RPW
@@ -401,8 +404,10 @@ __global__ __launch_bounds__(qkv_threads<RPW>()) void qkv_proj_kernel(LayerView 
     }
   }
   if (!finisher) return;
-  __syncthreads();
-  if (wave != 0) return;
+  if (wave != 0) {
+    __syncthreads();  // publishes this wave's rows in own[]; wave 0 polls before it meets them
+    return;
+  }
 
   // ---- the finishing part of the head: one wave, 4 dims a lane (D=128: both halves of the
   // wave hold the row; the lower one stores) ----
@@ -417,12 +422,10 @@ __global__ __launch_bounds__(qkv_threads<RPW>()) void qkv_proj_kernel(LayerView 
   float g[4] = {1.0f, 1.0f, 1.0f, 1.0f}, cs[4], sn[4];
   if (isq || isk) load4((isq ? a.q_gamma : a.k_gamma) + 4 * c, g);
   if (rope) row_tables(a.cos_tab, a.sin_tab, a.pos, a.rot_dim, c, cs, sn);
+  // the other workgroups' rows are polled before the barrier, under the sibling waves' rows
   float x[4];
   bool gave_up = false;
-  if (mine) {
-#pragma unroll
-    for (int e = 0; e < 4; e++) x[e] = own[4 * c + e - own0];
-  } else {
+  if (!mine) {
     const int spins = a.spin_limit > 0 ? a.spin_limit : (1 << 20);
     bool missing = true;
     for (int it = 0; it < spins && missing; it++) {
@@ -438,6 +441,11 @@ __global__ __launch_bounds__(qkv_threads<RPW>()) void qkv_proj_kernel(LayerView 
       if (missing) __builtin_amdgcn_s_sleep(1);
     }
     gave_up = missing;
+  }
+  __syncthreads();  // the sibling waves' rows in own[]
+  if (mine) {
+#pragma unroll
+    for (int e = 0; e < 4; e++) x[e] = own[4 * c + e - own0];
   }
   gave_up = __any(gave_up);
   // the empty marker back into the slots read, as soon as they are in registers (before the
