@@ -338,17 +338,17 @@ size_t qkv_proj_raw_floats(int heads, int D) { return (size_t)heads * D; }
 // Workgroup v owns rows [v RPW, v RPW + RPW) of the [Q heads | K heads | V heads] x D output.
 // The workgroup holding a head's last row finishes that head: its rows of the head stay in LDS,
 // its rows of the next head (RPW < D: a workgroup can straddle two heads) and every other
-// workgroup's rows go into the gather buffer; the finisher's first wave polls the head's earlier
+// workgroup's rows go into the gather buffer. The finisher's first wave polls the head's earlier
 // rows until none holds the empty marker (the data is the completion signal: no ticket, no store
-// acknowledgement to wait for) while its sibling waves finish their rows (it meets them at the
-// barrier only after the poll: 5.05 -> 4.85 us at the 8B shape), writes the marker back (written through: the next launch's
-// workgroups may run on another XCD), then normalizes, ropes and stores the row with the
-// prologue's arithmetic (bg_qkrow.h: bit-identical to bg_gemv_split followed by
-// bg_qkv_prologue). The rows a finisher waits on belong to lower workgroup indices, dispatched
-// before it, which finish on their own; the wait is still bounded (a finisher that gives up
-// stores NaN and raises the cache's error word). When the grid is a multiple of 8 and every
-// eighth of the rows is whole heads, blockIdx 8m + x is workgroup v = x (grid / 8) + m, so with
-// round-robin placement each XCD holds a run of whole heads and the raw rows stay in its L2.
+// acknowledgement to wait for) while its sibling waves finish their rows, and meets them at the
+// barrier only after the poll (5.05 -> 4.85 us at the 8B shape); it then writes the marker back
+// (written through: the next launch's workgroups may run on another XCD), normalizes, ropes and
+// stores the row with the prologue's arithmetic (bg_qkrow.h: bit-identical to bg_gemv_split
+// followed by bg_qkv_prologue). The rows a finisher waits on belong to lower workgroup indices,
+// dispatched before it, which finish on their own; the wait is still bounded (a finisher that
+// gives up stores NaN and raises the cache's error word). When the grid is a multiple of 8 and
+// every eighth of the rows is whole heads, blockIdx 8m + x is workgroup v = x (grid / 8) + m, so
+// with round-robin placement each XCD holds a run of whole heads and the raw rows stay in its L2.
 template <int D, int DT, int XM, int RPW>
 __global__ __launch_bounds__(qkv_threads<RPW>()) void qkv_proj_kernel(LayerView L, QkvProjArgs a) {
   constexpr int NT = qkv_threads<RPW>();
