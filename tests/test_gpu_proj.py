@@ -83,7 +83,20 @@ def test_qkv_proj_prologue_equals_unfused(dev, dtype, H, KV, D):
     (32, 8), (20, 2) and (24, 12) at D=128 run 24-row workgroups (heads across workgroup
     boundaries; 256 / 128 / 256 workgroups, the Q/K/V boundaries at different places), the
     others 32-row ones."""
-    K, pos = 4096, 777
+    _fused_equals_unfused(dtype, H, KV, D, 4096)
+
+
+@pytest.mark.parametrize("K", [5120, 13312])
+@pytest.mark.parametrize("H,KV,D", [(32, 8, 128), (8, 2, 256)])
+def test_qkv_proj_prologue_equals_unfused_long_rows(dev, H, KV, D, K):
+    """The same beyond the nibble table's 4096-weight rows: x staged in LDS (K = 5120, three
+    2048-weight tiles, the last one partial) and x read from memory (K = 13312), on 24-row and
+    32-row workgroups."""
+    _fused_equals_unfused("q8", H, KV, D, K)
+
+
+def _fused_equals_unfused(dtype, H, KV, D, K):
+    pos = 777
     rng, sign, sc, x, gq, gk = _qkv_case(dtype, H, KV, D, K, pos, seed=H + KV + D)
     w = _dev_weight(sign, sc, K, H * D, KV * D, KV * D)
     cos_d, sin_d, cos, sin = rope_dev(1e6, D, 1024)
