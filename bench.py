@@ -289,6 +289,9 @@ def profile_set(torch, E, W, names, n):
             fn, close = make_prologue(torch, E, W, W.C2, W.C2_S)
         elif name == "prologue_c5":
             fn, close = make_prologue(torch, E, W, W.C5, W.C5_PREFILL)
+        elif name == "proj":
+            run_q, run_o, close, _, _ = make_projections(torch, E)
+            fn = lambda: (run_q(), run_o())
         else:
             raise SystemExit(f"bench.py: unknown --profile-set entry {name}")
         for _ in range(n):
@@ -418,10 +421,11 @@ def onebit_bytes(N, K):
     return N * K // 8 + N * (K // 128) * 4 + K * 4 + N * 4
 
 
-def bench_projections(torch, E, steps, warmup, layers=36, HD=4096, H=32, KV=8, D=128):
+def make_projections(torch, E, layers=36, HD=4096, H=32, KV=8, D=128):
     """The decode projections on either side of attention in the Qwen3-8B shape (hidden 4096,
-    32 heads on 8 kv heads, head_dim 128), 36 distinct layers' weights (no cache reuse across
-    launches): the fused qkv projection + prologue into a q8 cache, and o_proj + residual."""
+    32 heads on 8 kv heads, head_dim 128), `layers` distinct layers' weights (no cache reuse
+    across launches): the fused qkv projection + prologue into a q8 cache, and o_proj +
+    residual. Returns (run_qkv, run_o, close, qkv_bytes, o_bytes); each run launches every layer."""
     rng = np.random.default_rng(7)
     dev = "cuda"
     Nq = (H + 2 * KV) * D
@@ -440,16 +444,23 @@ def bench_projections(torch, E, steps, warmup, layers=36, HD=4096, H=32, KV=8, D
     att = torch.randn(H * D, device=dev)
     q = torch.empty(1, H, D, device=dev)
     y = torch.empty(HD, device=dev)
-    us_q = graph_replay_us(torch, lambda: [E.qkv_proj_prologue(c, li, x, wq[li], H, ones, ones, 1e-6, cos, sin, D, 1000,
-                                                              1000, q_out=q) for li in range(layers)], steps, warmup) / layers
-    us_o = graph_replay_us(torch, lambda: [E.resid_mm(wo[li], att, h, y) for li in range(layers)], steps, warmup) / layers
-    c.close()
-    bq, bo = onebit_bytes(Nq, HD), onebit_bytes(HD, H * D)
+    run_q = lambda: [E.qkv_proj_prologue(c, li, x, wq[li], H, ones, ones, 1e-6, cos, sin, D, 1000, 1000, q_out=q)
+                     for li in range(layers)]
+    run_o = lambda: [E.resid_mm(wo[li], att, h, y) for li in range(layers)]
+    return run_q, run_o, c.close, onebit_bytes(Nq, HD), onebit_bytes(HD, H * D)
+
+
+def bench_projections(torch, E, steps, warmup, layers=36):
+    """The 1-bit decode projections (make_projections), graph-replayed, per launch."""
+    run_q, run_o, close, bq, bo = make_projections(torch, E, layers)
+    us_q = graph_replay_us(torch, run_q, steps, warmup) / layers
+    us_o = graph_replay_us(torch, run_o, steps, warmup) / layers
+    close()
     return {"qkv_proj_prologue": {"us": round(us_q, 2), "GBs": round(bq / us_q / 1e3, 1),
                                   "hbm_frac": round(bq / us_q / 1e3 / HBM_PEAK_GBS, 4), "bytes": bq},
             "o_proj_resid": {"us": round(us_o, 2), "GBs": round(bo / us_o / 1e3, 1),
                              "hbm_frac": round(bo / us_o / 1e3 / HBM_PEAK_GBS, 4), "bytes": bo},
-            "shape": f"hidden {HD}, {H} heads / {KV} kv heads x {D}, {layers} distinct layers"}
+            "shape": f"hidden 4096, 32 heads / 8 kv heads x 128, {layers} distinct layers"}
 
 
 def bench_read_floor(torch, steps, warmup, layers=36, nbytes=None, grids=(256, 512, 1024, 2048)):
@@ -509,7 +520,8 @@ def main():
     ap.add_argument("--profile-prefill", type=int, default=0,
                     help="run only the C2 and C5 prefill attention this many times each (for rocprofv3 --pmc)")
     ap.add_argument("--profile-set", default="", metavar="NAMES",
-                    help="comma list of decode_c5, decode_c4, verify_c4, prologue_c2, prologue_c5: run only these "
+                    help="comma list of decode_c5, decode_c4, verify_c4, prologue_c2, prologue_c5, proj (the 1-bit "
+                         "projections, every layer): run only these "
                          "kernels --profile-n times each (for rocprofv3 --pmc), print nothing else")
     ap.add_argument("--profile-n", type=int, default=20)
     ap.add_argument("--cpu-budget", type=float, default=12.0)
